@@ -1,0 +1,57 @@
+/*
+ * cmol_ext.h — internal entry points of libcmol (MI355X build) for test and
+ * benchmark harnesses.  Not part of the public API (include/cmol.h).
+ *
+ * The reference exposes the same capabilities only inside its library:
+ *   cmol__forward          reference src/model.c:176-276 (cmol_model_forward)
+ *   cmol__generate_ids     reference src/api.c:412-524 with token ids instead
+ *                          of text and the callback replaced by an id list
+ *   cmol__prefill          reference src/api.c:443-452 (prompt prefill loop)
+ *   cmol__decode_batch     no reference counterpart: lock-step decode of many
+ *                          sessions (the reference runs one thread per session)
+ *   cmol__session_fill_kv  no reference counterpart: synthetic KV contents of a
+ *                          given length, for long-context benchmarks
+ */
+#ifndef CMOL_EXT_H
+#define CMOL_EXT_H
+
+#include "cmol.h"
+#include "cmol_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One forward step of session s for `token` at position `pos`; copies the
+ * logits (vocab floats) when logits_out != NULL and returns the argmax id
+ * (>= 0) or a negative cmol_err_t.  Does not change the session's length. */
+int cmol__forward(cmol_session_t *s, int32_t token, int pos, float *logits_out);
+
+/* Prefill n prompt tokens at the session's current length, advancing it;
+ * returns the argmax of the last logits or a negative cmol_err_t. */
+int cmol__prefill(cmol_session_t *s, const int32_t *tokens, int n, float *logits_out);
+
+/* cmol_generate on token ids: appends the prompt, then samples until EOS,
+ * max_new_tokens or a full context; out receives the sampled ids (EOS
+ * included).  Returns the number written or a negative cmol_err_t. */
+int cmol__generate_ids(cmol_session_t *s, const int32_t *prompt, int n_prompt,
+                       const cmol_gen_params_t *params, int32_t *out, int out_cap);
+
+/* One lock-step decode step for n distinct sessions: session i consumes
+ * tokens[i] at its current length (then advanced by one); next[i] receives
+ * the argmax.  Returns CMOL_OK or a negative cmol_err_t. */
+int cmol__decode_batch(cmol_session_t *const *ss, const int32_t *tokens, int n,
+                       int32_t *next);
+
+/* Fill positions [0, n_tokens) of every layer of the session's KV cache with
+ * seeded synthetic values and set its length to n_tokens. */
+int cmol__session_fill_kv(cmol_session_t *s, int n_tokens, uint64_t seed);
+
+int cmol__session_length(const cmol_session_t *s);
+int cmol__session_slot(const cmol_session_t *s);
+cmolhip_model_t *cmol__device(cmol_model_t *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,166 @@
+/*
+ * cmol_hip.h — C ABI of the MI355X (gfx950) backend of libcmol.
+ *
+ * This is the platform backend that sits beside the reference's CPU
+ * platform layer (reference src/platform.h:21-63) and replaces the CPU
+ * kernel seam:
+ *   cmol_matmul_fn_t / cmol_kernels_t   reference src/cmol_internal.h:175-187
+ *   cmol_kernels_select                  reference src/quant.c:676-705
+ *   cmol_dequant_row                     reference src/quant.c:241-289
+ *   cmol_attn_forward                    reference src/attn.c:27-146
+ *   cmol_model_forward                   reference src/model.c:176-276
+ * Plain pointers and sizes only; every call returns a cmol_err_t value
+ * (0 = CMOL_OK, negative = error).  Device memory comes from one arena that
+ * is allocated once (cmolhip_ctx_create / cmolhip_model_create); no entry
+ * point allocates device memory afterwards.
+ */
+#ifndef CMOL_HIP_H
+#define CMOL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device context --------------------------------------------------- */
+typedef struct cmolhip_ctx cmolhip_ctx_t;
+
+/* Number of visible GPUs (0 when none or the runtime is unusable). */
+int cmolhip_device_count(void);
+/* Select `device`, create a stream and one device arena of `arena_bytes`. */
+int cmolhip_ctx_create(int device, size_t arena_bytes, cmolhip_ctx_t **out);
+void cmolhip_ctx_destroy(cmolhip_ctx_t *c);
+/* Bump-allocate from the arena (never calls the device allocator). */
+int cmolhip_alloc(cmolhip_ctx_t *c, size_t bytes, size_t align, void **dptr);
+size_t cmolhip_arena_used(const cmolhip_ctx_t *c);
+size_t cmolhip_arena_size(const cmolhip_ctx_t *c);
+int cmolhip_memcpy_h2d(cmolhip_ctx_t *c, void *dst, const void *src, size_t n);
+int cmolhip_memcpy_d2h(cmolhip_ctx_t *c, void *dst, const void *src, size_t n);
+int cmolhip_memcpy_d2d(cmolhip_ctx_t *c, void *dst, const void *src, size_t n);
+int cmolhip_synchronize(cmolhip_ctx_t *c);
+/* The context's hipStream_t, for callers that time work with HIP events. */
+void *cmolhip_stream(cmolhip_ctx_t *c);
+
+/* ---- quantised weights in the device layout -----------------------------
+ * GGUF block formats Q4_0 (2), Q5_0 (6) and Q8_0 (8) are repacked at upload
+ * into 16-row x 4-block tiles matched to the gfx950 MFMA operand layout
+ * (bit-preserving: codes and fp16 scales are moved, never re-quantised). */
+typedef struct {
+    void   *qs;          /* packed codes                                  */
+    void   *d;           /* fp16 scales                                   */
+    void   *qh;          /* Q5_0 fifth bits, NULL for other formats       */
+    int32_t dtype;       /* GGUF dtype id                                 */
+    int32_t rows;        /* output features                               */
+    int32_t cols;        /* input features (multiple of 32)               */
+    int32_t row_tiles;   /* ceil(rows / 16)                               */
+    int32_t block_quads; /* ceil(cols / 128)                              */
+    int32_t pad_;
+} cmolhip_qtensor_t;
+
+/* Device bytes a tensor needs (0 when dtype/shape is unsupported). */
+size_t cmolhip_qtensor_bytes(int dtype, int rows, int cols);
+
+#define CMOLHIP_PARTS_CONCAT     0 /* parts stacked row-wise              */
+#define CMOLHIP_PARTS_INTERLEAVE 1 /* two parts, rows alternate p0,p1,... */
+
+/* Upload raw GGUF rows (host memory) of `n_parts` tensors sharing dtype and
+ * cols into one device tensor.  `staging` is device scratch of at least
+ * staging_bytes >= largest part's raw size. */
+int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int n_parts,
+                           const void *const *parts, const int32_t *part_rows,
+                           int mode, void *staging, size_t staging_bytes,
+                           cmolhip_qtensor_t *out);
+
+/* fp32 dequantisation of the whole tensor to dout[rows][cols] (device),
+ * bit-identical to the reference's cmol_dequant_row row by row. */
+int cmolhip_dequant(cmolhip_ctx_t *c, const cmolhip_qtensor_t *t, float *dout);
+
+/* dy[n][rows] = W . dx[n][cols] for n activation vectors (fp32 accumulate).
+ * When norm_w != NULL each x is RMS-normalised first (weights norm_w[cols],
+ * epsilon eps).  n in 1..32.  Device pointers; runs on the context stream. */
+int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx,
+                 float *dy, int n, const float *norm_w, float eps);
+
+/* Reference kernel seam replacement (cmol_matmul_fn_t semantics on host
+ * memory): out[m][n] = A[m][k] . B[k][n], A raw GGUF rows.  Uses the
+ * context arena for the transient copies; fails with CMOL_ERR_OOM when the
+ * arena cannot hold them. */
+int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a,
+                        const float *b, int m, int k, int n, int dtype);
+
+/* Decode attention (reference src/attn.c:103-137) for `n` sessions whose
+ * fp32 or fp16 caches are stacked as [n][n_kv][max_ctx][d_head]; q is
+ * [n][n_heads*d_head] after RoPE, seqlen[n] (device int32) the number of
+ * positions attended, out [n][n_heads*d_head].  Device pointers. */
+int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q,
+                        const void *kcache, const void *vcache,
+                        const int32_t *seqlen, int n_heads, int n_kv,
+                        int d_head, int max_ctx, int kv_f16, float *out);
+
+/* ---- whole-model decode path ------------------------------------------- */
+typedef struct cmolhip_model cmolhip_model_t;
+
+typedef struct {
+    int32_t n_layers, n_heads, n_kv_heads, d_model, d_head, d_ffn, vocab;
+    int32_t max_ctx, max_sessions, no_rope_interval, kv_f16;
+    float   rope_base, rms_eps;
+} cmolhip_hparams_t;
+
+typedef struct {
+    const void *data;    /* host pointer into the mapped GGUF            */
+    int32_t dtype;       /* GGUF dtype id                                 */
+    int32_t rows, cols;  /* rows = GGUF shape[1] (out), cols = shape[0]  */
+} cmolhip_host_tensor_t;
+
+typedef struct {
+    cmolhip_host_tensor_t attn_norm, q, k, v, o, q_norm, k_norm,
+                          ffn_norm, gate, up, down;
+} cmolhip_layer_tensors_t;
+
+typedef struct {
+    cmolhip_hparams_t hp;
+    cmolhip_host_tensor_t embd, out_norm, lm_head;
+    const cmolhip_layer_tensors_t *layers;   /* [n_layers] */
+    const float *rope_table;                 /* [max_ctx][d_head/2][cos,sin] */
+} cmolhip_model_desc_t;
+
+/* Validate the description and report the device arena it needs. */
+int cmolhip_model_plan(const cmolhip_model_desc_t *desc, size_t *device_bytes);
+/* Allocate the arena once, upload every tensor, create per-session streams
+ * and capture each session's decode graph.  Nothing is allocated later. */
+int cmolhip_model_create(const cmolhip_model_desc_t *desc, int device,
+                         cmolhip_model_t **out);
+void cmolhip_model_destroy(cmolhip_model_t *m);
+cmolhip_ctx_t *cmolhip_model_ctx(cmolhip_model_t *m);
+
+/* One decode step of session `slot` (reference cmol_model_forward):
+ * token at position pos.  logits_host (vocab floats) and argmax are
+ * optional outputs; argmax is the first index of the maximum logit. */
+int cmolhip_decode(cmolhip_model_t *m, int slot, int32_t token, int32_t pos,
+                   float *logits_host, int32_t *argmax);
+/* Lock-step decode of n sessions (distinct slots, each at its own pos). */
+int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots,
+                         const int32_t *tokens, const int32_t *pos,
+                         float *logits_host, int32_t *argmax);
+/* Prompt of n tokens at positions pos0.. into session `slot`; outputs as in
+ * cmolhip_decode for the last prompt token. */
+int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n,
+                    int32_t pos0, float *logits_host, int32_t *argmax);
+
+/* KV cache of one session and layer in the reference layout
+ * [pos][n_kv][d_head] fp32 for positions [0, n). */
+int cmolhip_kv_download(cmolhip_model_t *m, int slot, int layer, int n,
+                        float *k_out, float *v_out);
+int cmolhip_kv_upload(cmolhip_model_t *m, int slot, int layer, int n,
+                      const float *k_in, const float *v_in);
+/* Fill positions [0, n) of every layer with seeded synthetic values. */
+int cmolhip_kv_fill_synthetic(cmolhip_model_t *m, int slot, int n, uint64_t seed);
+/* Stream of a session slot (hipStream_t), for event timing. */
+void *cmolhip_session_stream(cmolhip_model_t *m, int slot);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,179 @@
+// common.h — shared device types, the tiled weight layout and the
+// per-format code-to-f16 decoders used by every gfx950 kernel of libcmol.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q5_0 = 6, DT_Q8_0 = 8 };
+
+// ---------------------------------------------------------------------------
+// Tiled weight layout ("quad tiles").
+//
+// A GGUF block tensor of M rows x K cols (nb = K/32 blocks per row) is stored
+// as RT = ceil(M/16) row tiles x BQ = ceil(nb/4) block quads.  Within a
+// (tile t, quad q) cell every one of the 64 lanes of a wavefront owns the
+// codes it feeds to one v_mfma_f32_16x16x32_f16 as its B operand:
+//   lane l  ->  weight row 16t + (l % 16), k-group g = l / 16
+//   Q4_0/Q5_0: 16 bytes = dword g of the 16-byte nibble array of blocks
+//              4q..4q+3 (4 bytes per block)
+//   Q8_0:      32 bytes = bytes 8g..8g+7 of the 32 int8 codes of blocks
+//              4q..4q+3 (8 bytes per block)
+// so one wave-wide 16-byte (or 2x16-byte) load per lane moves a contiguous
+// 1 KiB (2 KiB).  Scales: 16 rows x 4 blocks fp16 per cell (128 bytes),
+// entry [row % 16][block % 4].  Q5_0 fifth bits: one dword per lane per cell,
+// byte (block % 4) holding the 8 fifth bits of the lane's 8 codes in pair
+// order (see deq_q5).  Rows beyond M and blocks beyond nb are zero-filled.
+//
+// k order inside a block for lane group g, element e (the same permutation is
+// applied to the activation operand, so the MFMA contraction is unchanged):
+//   Q4_0/Q5_0: e -> (e>=4 ? 16 : 0) + 4g + {0,2,1,3}[e&3]
+//   Q8_0:      e -> 8g + e
+// ---------------------------------------------------------------------------
+
+template <int DT> struct QFmt;
+template <> struct QFmt<DT_Q4_0> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 18; };
+template <> struct QFmt<DT_Q5_0> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 22; };
+template <> struct QFmt<DT_Q8_0> { static constexpr int LANE_BYTES = 32, BLOCK_BYTES = 34; };
+
+__host__ __device__ inline int lane_bytes_of(int dt) { return dt == DT_Q8_0 ? 32 : 16; }
+__host__ __device__ inline int block_bytes_of(int dt)
+{
+    return dt == DT_Q4_0 ? 18 : dt == DT_Q5_0 ? 22 : dt == DT_Q8_0 ? 34 : 0;
+}
+
+// position (0..31) inside a block of element e for lane group g
+__host__ __device__ inline int kmap(int dt, int g, int e)
+{
+    if (dt == DT_Q8_0) return 8 * g + e;
+    const int sub[4] = {0, 2, 1, 3};
+    return (e >= 4 ? 16 : 0) + 4 * g + sub[e & 3];
+}
+
+__device__ inline f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+__device__ inline f16x8 pack8(f16x2 a, f16x2 b, f16x2 c, f16x2 d)
+{
+    f16x4 lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+    f16x4 hi = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Codes -> exact small integers in f16.  0x6400 | n is the f16 value 1024+n
+// for n < 1024, so OR-ing a nibble/byte under that exponent and subtracting
+// the bias in packed f16 yields the signed code exactly.
+
+// Q4_0: dword D holds bytes b0..b3; value = nibble - 8.
+__device__ inline f16x8 deq_q4(uint32_t D)
+{
+    const f16x2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    uint32_t p0 = (D & 0x000F000Fu) | 0x64006400u;
+    uint32_t p1 = ((D >> 8) & 0x000F000Fu) | 0x64006400u;
+    uint32_t p2 = ((D >> 4) & 0x000F000Fu) | 0x64006400u;
+    uint32_t p3 = ((D >> 12) & 0x000F000Fu) | 0x64006400u;
+    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) + bias, as_h2(p3) + bias);
+}
+
+// Q5_0: nibbles as Q4_0 plus fifth bits; hb = the lane's byte for this block
+// (bit p: low element of pair p, bit 4+p: high element of pair p).
+// value = (nibble | fifth << 4) - 16.
+__device__ inline f16x8 deq_q5(uint32_t D, uint32_t hb)
+{
+    const f16x2 bias = {(_Float16)-1040.0f, (_Float16)-1040.0f};
+    uint32_t hs = ((hb & 0x0Fu) << 4) | ((hb & 0xF0u) << 16);
+    uint32_t p0 = (D & 0x000F000Fu) | 0x64006400u | (hs & 0x00100010u);
+    uint32_t p1 = ((D >> 8) & 0x000F000Fu) | 0x64006400u | ((hs >> 1) & 0x00100010u);
+    uint32_t p2 = ((D >> 4) & 0x000F000Fu) | 0x64006400u | ((hs >> 2) & 0x00100010u);
+    uint32_t p3 = ((D >> 12) & 0x000F000Fu) | 0x64006400u | ((hs >> 3) & 0x00100010u);
+    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) + bias, as_h2(p3) + bias);
+}
+
+// Q8_0: two dwords of int8 codes; flip the sign bit (b+128 in 0..255),
+// place each byte under the 0x64 exponent byte, subtract 1152.
+__device__ inline f16x8 deq_q8(uint32_t D0, uint32_t D1)
+{
+    const f16x2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    D0 ^= 0x80808080u;
+    D1 ^= 0x80808080u;
+    uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, D0, 0x04010400u);
+    uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, D0, 0x04030402u);
+    uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, D1, 0x04010400u);
+    uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, D1, 0x04030402u);
+    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) + bias, as_h2(p3) + bias);
+}
+
+// Decoded codes of block bi (0..3) of a quad from a lane's loaded data.
+template <int DT>
+__device__ inline f16x8 deq_block(const u32x4 c0, const u32x4 c1, uint32_t h, int bi)
+{
+    if constexpr (DT == DT_Q4_0) {
+        return deq_q4(c0[bi]);
+    } else if constexpr (DT == DT_Q5_0) {
+        return deq_q5(c0[bi], (h >> (8 * bi)) & 0xFFu);
+    } else {
+        uint32_t a = bi < 2 ? c0[2 * bi] : c1[2 * bi - 4];
+        uint32_t b = bi < 2 ? c0[2 * bi + 1] : c1[2 * bi - 3];
+        return deq_q8(a, b);
+    }
+}
+
+// IEEE half -> float, exact, from bits (NaN payload moved as mantissa<<13).
+__device__ inline float f16_bits_to_f32(uint32_t h)
+{
+    uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, f = h & 0x3FFu, bits;
+    if (e == 31u) bits = sign | 0x7F800000u | (f << 13);
+    else if (e) bits = sign | ((e + 112u) << 23) | (f << 13);
+    else if (!f) bits = sign;
+    else {
+        int lead = 31 - __builtin_clz(f);
+        bits = sign | ((uint32_t)(lead + 103) << 23) | (((f << (10 - lead)) & 0x3FFu) << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// d * q with the result an x86 SSE multiply gives for special scales:
+// NaN scale -> the quieted NaN itself; inf * 0 -> the x86 default NaN.
+__device__ inline float mul_scale_x86(float d, float q)
+{
+    uint32_t db = __float_as_uint(d);
+    if ((db & 0x7F800000u) == 0x7F800000u) {
+        if (db & 0x007FFFFFu) return __uint_as_float(db | 0x00400000u);
+        if (q == 0.0f) return __uint_as_float(0xFFC00000u);
+    }
+    return d * q;
+}
+
+// ---- reductions ------------------------------------------------------------
+__device__ inline float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ inline float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Orderable 64-bit key: larger float wins, ties go to the smaller index,
+// NaN never wins.
+__device__ inline unsigned long long argmax_key(float v, uint32_t idx)
+{
+    uint32_t u = __float_as_uint(v);
+    uint32_t k = (v != v) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    return ((unsigned long long)k << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+__host__ __device__ inline uint32_t argmax_index(unsigned long long key)
+{
+    return 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull);
+}

@@ -1,0 +1,119 @@
+// misc.hip — fills and KV-cache conversions used by load, tests and benches.
+#include "common.h"
+#include "kernels.h"
+
+__global__ void k_fill_f32(float *p, size_t n, float v)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+int launch_fill_f32(float *p, size_t n, float v, hipStream_t s)
+{
+    if (!n) return 0;
+    unsigned grid = (unsigned)((n + 255) / 256);
+    if (grid > 65535u * 16u) grid = 65535u * 16u;
+    hipLaunchKernelGGL(k_fill_f32, dim3(grid), dim3(256), 0, s, p, n, v);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+__device__ inline uint64_t mix64d(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Synthetic cache contents ~U(-1,1) for positions [0, n) of one layer slice
+// [n_kv][max_ctx][d_head]; layers are handled by the caller's loop.
+__global__ void k_kv_synth(void *kc, void *vc, int n_kv, int max_ctx, int d_head,
+                           int n, int kv_f16, uint64_t seed)
+{
+    size_t total = (size_t)n_kv * n * d_head;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        int dd = (int)(i % d_head);
+        size_t r = i / d_head;
+        int pos = (int)(r % n), h = (int)(r / n);
+        size_t idx = ((size_t)h * max_ctx + pos) * d_head + dd;
+        uint64_t z = mix64d(seed ^ mix64d(idx));
+        float a = (float)(int32_t)(z & 0xFFFFFF) * (1.0f / 8388608.0f) - 1.0f;
+        float b = (float)(int32_t)((z >> 32) & 0xFFFFFF) * (1.0f / 8388608.0f) - 1.0f;
+        if (kv_f16) {
+            ((_Float16 *)kc)[idx] = (_Float16)a;
+            ((_Float16 *)vc)[idx] = (_Float16)b;
+        } else {
+            ((float *)kc)[idx] = a;
+            ((float *)vc)[idx] = b;
+        }
+    }
+}
+
+int launch_kv_synth(void *kc, void *vc, int n_kv, int max_ctx, int d_head,
+                    int n_tokens, int kv_f16, uint64_t seed, hipStream_t s)
+{
+    size_t total = (size_t)n_kv * n_tokens * d_head;
+    if (!total) return 0;
+    unsigned grid = (unsigned)((total + 255) / 256);
+    if (grid > 65535u * 4u) grid = 65535u * 4u;
+    hipLaunchKernelGGL(k_kv_synth, dim3(grid), dim3(256), 0, s, kc, vc, n_kv, max_ctx,
+                       d_head, n_tokens, kv_f16, seed);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// Device cache slice [n_kv][max_ctx][d_head] -> reference layout
+// [pos][n_kv][d_head] fp32 for positions [0, n).
+__global__ void k_kv_to_ref(const void *src, float *dst, int n_kv, int max_ctx, int d_head,
+                            int n, int kv_f16)
+{
+    size_t total = (size_t)n * n_kv * d_head;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        int dd = (int)(i % d_head);
+        size_t r = i / d_head;
+        int h = (int)(r % n_kv), pos = (int)(r / n_kv);
+        size_t sidx = ((size_t)h * max_ctx + pos) * d_head + dd;
+        dst[i] = kv_f16 ? (float)((const _Float16 *)src)[sidx] : ((const float *)src)[sidx];
+    }
+}
+
+__global__ void k_kv_from_ref(const float *src, void *dst, int n_kv, int max_ctx, int d_head,
+                              int n, int kv_f16)
+{
+    size_t total = (size_t)n * n_kv * d_head;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        int dd = (int)(i % d_head);
+        size_t r = i / d_head;
+        int h = (int)(r % n_kv), pos = (int)(r / n_kv);
+        size_t didx = ((size_t)h * max_ctx + pos) * d_head + dd;
+        if (kv_f16) ((_Float16 *)dst)[didx] = (_Float16)src[i];
+        else ((float *)dst)[didx] = src[i];
+    }
+}
+
+int launch_kv_convert(const void *src, float *dst, int n_kv, int max_ctx, int d_head,
+                      int n, int kv_f16, int to_ref, hipStream_t s)
+{
+    (void)to_ref;
+    size_t total = (size_t)n * n_kv * d_head;
+    if (!total) return 0;
+    unsigned grid = (unsigned)((total + 255) / 256);
+    if (grid > 65535u * 4u) grid = 65535u * 4u;
+    hipLaunchKernelGGL(k_kv_to_ref, dim3(grid), dim3(256), 0, s, src, dst, n_kv, max_ctx,
+                       d_head, n, kv_f16);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_kv_import(const float *src, void *dst, int n_kv, int max_ctx, int d_head, int n,
+                     int kv_f16, hipStream_t s)
+{
+    size_t total = (size_t)n * n_kv * d_head;
+    if (!total) return 0;
+    unsigned grid = (unsigned)((total + 255) / 256);
+    if (grid > 65535u * 4u) grid = 65535u * 4u;
+    hipLaunchKernelGGL(k_kv_from_ref, dim3(grid), dim3(256), 0, s, src, dst, n_kv, max_ctx,
+                       d_head, n, kv_f16);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}

@@ -1,0 +1,173 @@
+/*
+ * sampler.c — token selection on the host (reference src/sampler.c).
+ *
+ * Greedy: first index of the maximum logit (src/sampler.c:199-204).
+ * Otherwise: temperature scaling, softmax, optional top-k (min-heap of at most
+ * 512) and top-p nucleus, then one draw from xoshiro256** seeded by
+ * splitmix64 (src/sampler.c:37-75), so the same seed selects the same token as
+ * the reference.  The repetition penalty divides positive / multiplies
+ * non-positive logits, once per occurrence in the window (src/sampler.c:171-184).
+ */
+#include "internal.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+static inline uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+/* xoshiro256** step (Blackman & Vigna). */
+uint64_t cmol_rng_next(uint64_t s[4])
+{
+    const uint64_t out = rotl(s[1] * 5u, 7) * 9u;
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl(s[3], 45);
+    return out;
+}
+
+/* splitmix64 (Steele, Lea, Flood) used to expand the 32-bit seed. */
+static uint64_t splitmix(uint64_t *x)
+{
+    uint64_t z = (*x += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void cmol_rng_seed(uint64_t st[4], unsigned int seed)
+{
+    uint64_t x;
+    if (seed == 0) {
+        static uint64_t counter = 0;
+        x = (uint64_t)time(NULL) ^ (++counter * 6364136223846793005ull) ^ (uint64_t)(uintptr_t)st;
+        if (!x) x = 0xDEADBEEFCAFEBABEull;
+    } else {
+        x = (uint64_t)seed;
+    }
+    for (int i = 0; i < 4; i++) st[i] = splitmix(&x);
+}
+
+/* Uniform float in [0,1): 23 random mantissa bits under exponent 127. */
+static float rng_unit(uint64_t st[4])
+{
+    uint32_t bits = 0x3F800000u | (uint32_t)(cmol_rng_next(st) >> 41);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f - 1.0f;
+}
+
+void cmol_apply_repeat_penalty(float *logits, int vocab, const int32_t *tokens, int n, float penalty)
+{
+    if (penalty <= 1.0f || !logits || !tokens || n <= 0) return;
+    for (int i = 0; i < n; i++) {
+        int32_t id = tokens[i];
+        if (id < 0 || id >= vocab) continue;
+        logits[id] = logits[id] > 0.0f ? logits[id] / penalty : logits[id] * penalty;
+    }
+}
+
+static int32_t argmax_first(const float *x, int n)
+{
+    int32_t best = 0;
+    for (int i = 1; i < n; i++) if (x[i] > x[best]) best = i;
+    return best;
+}
+
+static void softmax_inplace(float *x, int n)
+{
+    float mx = x[0], sum = 0.0f;
+    for (int i = 1; i < n; i++) if (x[i] > mx) mx = x[i];
+    for (int i = 0; i < n; i++) { x[i] = expf(x[i] - mx); sum += x[i]; }
+    sum = 1.0f / sum;
+    for (int i = 0; i < n; i++) x[i] *= sum;
+}
+
+typedef struct { float p; int32_t id; } cand_t;
+#define TOPK_MAX 512
+
+static void heap_down(cand_t *h, int i, int n)
+{
+    for (;;) {
+        int m = i, l = 2 * i + 1, r = l + 1;
+        if (l < n && h[l].p < h[m].p) m = l;
+        if (r < n && h[r].p < h[m].p) m = r;
+        if (m == i) return;
+        cand_t t = h[i]; h[i] = h[m]; h[m] = t;
+        i = m;
+    }
+}
+
+static void heap_up(cand_t *h, int i)
+{
+    while (i > 0) {
+        int p = (i - 1) / 2;
+        if (h[p].p <= h[i].p) return;
+        cand_t t = h[i]; h[i] = h[p]; h[p] = t;
+        i = p;
+    }
+}
+
+static int by_p_desc(const void *a, const void *b)
+{
+    float x = ((const cand_t *)a)->p, y = ((const cand_t *)b)->p;
+    return x < y ? 1 : x > y ? -1 : 0;
+}
+
+int32_t cmol_sample(float *logits, int V, const cmol_gen_params_t *prm, uint64_t *rng)
+{
+    if (!logits || V <= 0) return 0;
+    if (!prm || prm->temperature == 0.0f) return argmax_first(logits, V);
+    const float inv_t = 1.0f / prm->temperature;
+    for (int i = 0; i < V; i++) logits[i] *= inv_t;
+    softmax_inplace(logits, V);
+    const int use_k = prm->top_k > 0 && prm->top_k < V;
+    const int use_p = prm->top_p > 0.0f && prm->top_p < 1.0f;
+    if (!use_k && !use_p) {
+        if (!rng) return argmax_first(logits, V);
+        float r = rng_unit(rng), acc = 0.0f;
+        for (int i = 0; i < V - 1; i++) {
+            acc += logits[i];
+            if (r < acc) return i;
+        }
+        return V - 1;
+    }
+    cand_t heap[TOPK_MAX];
+    int k = use_k ? prm->top_k : V;
+    if (k > TOPK_MAX) k = TOPK_MAX;
+    int n = 0;
+    for (int i = 0; i < V; i++) {
+        if (n < k) {
+            heap[n].p = logits[i];
+            heap[n].id = i;
+            heap_up(heap, n++);
+        } else if (logits[i] > heap[0].p) {
+            heap[0].p = logits[i];
+            heap[0].id = i;
+            heap_down(heap, 0, k);
+        }
+    }
+    qsort(heap, (size_t)n, sizeof(cand_t), by_p_desc);
+    int nuc = n;
+    if (use_p) {
+        float cum = 0.0f;
+        for (int i = 0; i < n; i++) {
+            cum += heap[i].p;
+            if (cum >= prm->top_p) { nuc = i + 1; break; }
+        }
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < nuc; i++) sum += heap[i].p;
+    if (!rng || sum <= 0.0f) return heap[0].id;
+    float r = rng_unit(rng) * sum, acc = 0.0f;
+    for (int i = 0; i < nuc; i++) {
+        acc += heap[i].p;
+        if (r < acc) return heap[i].id;
+    }
+    return heap[nuc - 1].id;
+}

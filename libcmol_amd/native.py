@@ -1,0 +1,307 @@
+"""ctypes bindings of libcmol.so: the public C API (include/cmol.h), the gfx950
+backend C ABI (include/cmol_hip.h) and the harness entry points
+(include/cmol_ext.h).
+
+The library is required: nothing here falls back to a CPU path.  Loading fails
+loudly when the in-tree build is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import _paths
+
+P = C.c_void_p
+I32 = C.c_int32
+CMOL_OK, CMOL_ERR_OOM, CMOL_ERR_IO, CMOL_ERR_INVALID, CMOL_ERR_UNSUPPORTED = 0, -1, -2, -3, -4
+CMOL_ERR_NO_SESSION, CMOL_ERR_ARGS, CMOL_ERR_CTX_FULL, CMOL_ERR_TRUNC = -5, -6, -7, -8
+
+LOG_FN = C.CFUNCTYPE(None, C.c_int, C.c_char_p, C.c_void_p)
+TOKEN_CB = C.CFUNCTYPE(C.c_int, C.c_char_p, C.c_size_t, C.c_int, C.c_void_p)
+
+
+class Config(C.Structure):
+    _fields_ = [("max_ctx", C.c_int), ("max_sessions", C.c_int), ("prefill_chunk", C.c_int),
+                ("log_fn", LOG_FN), ("log_ud", C.c_void_p)]
+
+
+class GenParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int),
+                ("max_new_tokens", C.c_int), ("seed", C.c_uint), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", C.c_int)]
+
+
+def default_params(**kw) -> GenParams:
+    p = GenParams(0.8, 0.95, 40, 256, 0, 1.1, 64)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def greedy_params(max_new: int, **kw) -> GenParams:
+    return default_params(temperature=0.0, repeat_penalty=1.0, max_new_tokens=max_new, **kw)
+
+
+class QTensor(C.Structure):
+    _fields_ = [("qs", P), ("d", P), ("qh", P), ("dtype", I32), ("rows", I32), ("cols", I32),
+                ("row_tiles", I32), ("block_quads", I32), ("pad_", I32)]
+
+
+# (name, restype, argtypes) of every exported entry point declared in include/*.h
+SIGNATURES = [
+    # cmol.h
+    ("cmol_load", P, [C.c_char_p, C.POINTER(Config), C.POINTER(C.c_int)]),
+    ("cmol_free", None, [P]),
+    ("cmol_session_acquire", P, [P]),
+    ("cmol_session_release", None, [P]),
+    ("cmol_session_reset", None, [P]),
+    ("cmol_generate", C.c_int, [P, C.c_char_p, C.POINTER(GenParams), TOKEN_CB, P]),
+    ("cmol_encode", C.c_int, [P, C.c_char_p, P, C.c_int]),
+    ("cmol_decode_token", C.c_char_p, [P, I32]),
+    ("cmol_strerror", C.c_char_p, [C.c_int]),
+    ("cmol_version", C.c_char_p, []),
+    ("cmol_arena_estimate", C.c_size_t, [C.c_char_p, C.POINTER(Config)]),
+    ("cmol_format_chatml", C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_size_t]),
+    ("cmol_format_chatml_turn", C.c_int, [C.c_char_p, C.c_char_p, C.c_size_t]),
+    # cmol_hip.h
+    ("cmolhip_device_count", C.c_int, []),
+    ("cmolhip_ctx_create", C.c_int, [C.c_int, C.c_size_t, C.POINTER(P)]),
+    ("cmolhip_ctx_destroy", None, [P]),
+    ("cmolhip_alloc", C.c_int, [P, C.c_size_t, C.c_size_t, C.POINTER(P)]),
+    ("cmolhip_arena_used", C.c_size_t, [P]),
+    ("cmolhip_arena_size", C.c_size_t, [P]),
+    ("cmolhip_memcpy_h2d", C.c_int, [P, P, P, C.c_size_t]),
+    ("cmolhip_memcpy_d2h", C.c_int, [P, P, P, C.c_size_t]),
+    ("cmolhip_memcpy_d2d", C.c_int, [P, P, P, C.c_size_t]),
+    ("cmolhip_synchronize", C.c_int, [P]),
+    ("cmolhip_stream", P, [P]),
+    ("cmolhip_qtensor_bytes", C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+    ("cmolhip_qtensor_upload", C.c_int, [P, C.c_int, C.c_int, C.c_int, C.POINTER(P),
+                                         C.POINTER(I32), C.c_int, P, C.c_size_t,
+                                         C.POINTER(QTensor)]),
+    ("cmolhip_dequant", C.c_int, [P, C.POINTER(QTensor), P]),
+    ("cmolhip_gemm", C.c_int, [P, C.POINTER(QTensor), P, P, C.c_int, P, C.c_float]),
+    ("cmolhip_matmul_host", C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("cmolhip_attn_decode", C.c_int, [P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, C.c_int, P]),
+    ("cmolhip_model_plan", C.c_int, [P, C.POINTER(C.c_size_t)]),
+    ("cmolhip_model_create", C.c_int, [P, C.c_int, C.POINTER(P)]),
+    ("cmolhip_model_destroy", None, [P]),
+    ("cmolhip_model_ctx", P, [P]),
+    ("cmolhip_decode", C.c_int, [P, C.c_int, I32, I32, P, P]),
+    ("cmolhip_decode_batch", C.c_int, [P, C.c_int, P, P, P, P, P]),
+    ("cmolhip_prefill", C.c_int, [P, C.c_int, P, C.c_int, I32, P, P]),
+    ("cmolhip_kv_download", C.c_int, [P, C.c_int, C.c_int, C.c_int, P, P]),
+    ("cmolhip_kv_upload", C.c_int, [P, C.c_int, C.c_int, C.c_int, P, P]),
+    ("cmolhip_kv_fill_synthetic", C.c_int, [P, C.c_int, C.c_int, C.c_uint64]),
+    ("cmolhip_session_stream", P, [P, C.c_int]),
+    # cmol_ext.h
+    ("cmol__forward", C.c_int, [P, I32, C.c_int, P]),
+    ("cmol__prefill", C.c_int, [P, P, C.c_int, P]),
+    ("cmol__generate_ids", C.c_int, [P, P, C.c_int, C.POINTER(GenParams), P, C.c_int]),
+    ("cmol__decode_batch", C.c_int, [P, P, C.c_int, P]),
+    ("cmol__session_fill_kv", C.c_int, [P, C.c_int, C.c_uint64]),
+    ("cmol__session_length", C.c_int, [P]),
+    ("cmol__session_slot", C.c_int, [P]),
+    ("cmol__device", P, [P]),
+]
+
+_lib = None
+
+
+def lib_path() -> str:
+    return _paths.lib_path("libcmol.so")
+
+
+def lib():
+    """The loaded libcmol.so (raises when the in-tree build is missing)."""
+    global _lib
+    if _lib is None:
+        path = lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build()")
+        L = C.CDLL(path)
+        for name, res, args in SIGNATURES:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "call"):
+    if rc < 0:
+        msg = lib().cmol_strerror(rc).decode()
+        raise RuntimeError(f"{what} failed: {rc} ({msg})")
+    return rc
+
+
+def device_count() -> int:
+    return lib().cmolhip_device_count()
+
+
+def ptr(a: np.ndarray):
+    return C.c_void_p(a.ctypes.data)
+
+
+# ---------------------------------------------------------------------------
+# Device context helpers (kernel-level tests and benches)
+# ---------------------------------------------------------------------------
+class Ctx:
+    def __init__(self, arena_bytes: int, device: int = 0):
+        h = C.c_void_p()
+        check(lib().cmolhip_ctx_create(device, arena_bytes, C.byref(h)), "cmolhip_ctx_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().cmolhip_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def alloc(self, nbytes: int, align: int = 256) -> int:
+        p = C.c_void_p()
+        check(lib().cmolhip_alloc(self.h, nbytes, align, C.byref(p)), "cmolhip_alloc")
+        return p.value
+
+    def h2d(self, dptr: int, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        check(lib().cmolhip_memcpy_h2d(self.h, C.c_void_p(dptr), ptr(a), a.nbytes), "h2d")
+
+    def d2h(self, dptr: int, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        check(lib().cmolhip_memcpy_d2h(self.h, ptr(out), C.c_void_p(dptr), out.nbytes), "d2h")
+        return out
+
+    def upload(self, a: np.ndarray) -> int:
+        a = np.ascontiguousarray(a)
+        d = self.alloc(max(a.nbytes, 1))
+        self.h2d(d, a)
+        return d
+
+    def qtensor(self, raw_parts, dtype: int, cols: int, rows, mode: int = 0,
+                staging_bytes: int | None = None) -> QTensor:
+        parts = [np.ascontiguousarray(p, np.uint8) for p in raw_parts]
+        staging_bytes = staging_bytes or max(p.nbytes for p in parts)
+        stg = self.alloc(staging_bytes)
+        arr_p = (C.c_void_p * len(parts))(*[p.ctypes.data for p in parts])
+        arr_r = (I32 * len(parts))(*rows)
+        t = QTensor()
+        check(lib().cmolhip_qtensor_upload(self.h, dtype, cols, len(parts), arr_p, arr_r, mode,
+                                           C.c_void_p(stg), staging_bytes, C.byref(t)), "upload")
+        return t
+
+    def dequant(self, t: QTensor) -> np.ndarray:
+        d = self.alloc(t.rows * t.cols * 4)
+        check(lib().cmolhip_dequant(self.h, C.byref(t), C.c_void_p(d)), "dequant")
+        return self.d2h(d, (t.rows, t.cols), np.float32)
+
+    def gemm(self, t: QTensor, x: np.ndarray, norm_w: np.ndarray | None = None,
+             eps: float = 1e-5) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, t.cols)
+        n = x.shape[0]
+        dx = self.upload(x)
+        dy = self.alloc(n * t.rows * 4)
+        dn = self.upload(np.ascontiguousarray(norm_w, np.float32)) if norm_w is not None else None
+        check(lib().cmolhip_gemm(self.h, C.byref(t), C.c_void_p(dx), C.c_void_p(dy), n,
+                                 C.c_void_p(dn) if dn else None, eps), "gemm")
+        check(lib().cmolhip_synchronize(self.h), "sync")
+        return self.d2h(dy, (n, t.rows), np.float32)
+
+    def stream(self):
+        return lib().cmolhip_stream(self.h)
+
+
+# ---------------------------------------------------------------------------
+# Model / sessions (public API + harness entry points)
+# ---------------------------------------------------------------------------
+class Model:
+    def __init__(self, path: str, max_ctx: int = 0, max_sessions: int = 1, log: bool = False):
+        self._logs = []
+        self._logfn = LOG_FN(lambda lvl, msg, ud: self._logs.append(msg.decode()))
+        cfg = Config(max_ctx, max_sessions, 512, self._logfn if log else LOG_FN(), None)
+        err = C.c_int(0)
+        self.h = lib().cmol_load(path.encode(), C.byref(cfg), C.byref(err))
+        if not self.h:
+            raise RuntimeError(f"cmol_load({path}) failed: {err.value} "
+                               f"({lib().cmol_strerror(err.value).decode()})")
+        self.path = path
+
+    def close(self):
+        if self.h:
+            lib().cmol_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def acquire(self) -> "Session":
+        s = lib().cmol_session_acquire(self.h)
+        return Session(self, s) if s else None
+
+    @property
+    def device(self):
+        return lib().cmol__device(self.h)
+
+
+class Session:
+    def __init__(self, model: Model, handle):
+        self.model = model
+        self.h = handle
+
+    def release(self):
+        lib().cmol_session_release(self.h)
+
+    def reset(self):
+        lib().cmol_session_reset(self.h)
+
+    @property
+    def length(self) -> int:
+        return lib().cmol__session_length(self.h)
+
+    @property
+    def slot(self) -> int:
+        return lib().cmol__session_slot(self.h)
+
+    def forward(self, token: int, pos: int, vocab: int | None = None):
+        logits = np.zeros(vocab, np.float32) if vocab else None
+        r = check(lib().cmol__forward(self.h, int(token), int(pos),
+                                      ptr(logits) if logits is not None else None), "forward")
+        return r, logits
+
+    def prefill(self, tokens, vocab: int | None = None):
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.zeros(vocab, np.float32) if vocab else None
+        r = check(lib().cmol__prefill(self.h, ptr(t), t.size,
+                                      ptr(logits) if logits is not None else None), "prefill")
+        return r, logits
+
+    def generate_ids(self, prompt, params: GenParams, cap: int) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(cap, np.int32)
+        n = check(lib().cmol__generate_ids(self.h, ptr(p), p.size, C.byref(params), ptr(out), cap),
+                  "generate_ids")
+        return out[:n]
+
+    def fill_kv(self, n_tokens: int, seed: int = 7):
+        check(lib().cmol__session_fill_kv(self.h, n_tokens, seed), "fill_kv")
+
+
+def decode_batch(sessions, tokens) -> np.ndarray:
+    n = len(sessions)
+    arr = (C.c_void_p * n)(*[s.h for s in sessions])
+    t = np.ascontiguousarray(tokens, np.int32)
+    out = np.zeros(n, np.int32)
+    check(lib().cmol__decode_batch(arr, ptr(t), n, ptr(out)), "decode_batch")
+    return out

@@ -1,0 +1,27 @@
+"""Seeded raw GGUF blocks and activations for kernel tests."""
+import numpy as np
+
+BLOCK_BYTES = {2: 18, 6: 22, 8: 34}
+SPECIAL_SCALES = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x0400, 0x3C00, 0xBC00,
+                           0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x7C01, 0xFD55, 0x1234, 0x0200],
+                          np.uint16)
+
+
+def f16bits(x):
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def random_blocks(dtype, rows, cols, seed, special=False, scale_lo=0.002, scale_hi=0.05):
+    """Raw rows of a GGUF block tensor: random codes, fp16 scales in
+    [scale_lo, scale_hi) with random sign (or the IEEE special set)."""
+    rng = np.random.default_rng(seed)
+    nb = cols // 32
+    bb = BLOCK_BYTES[dtype]
+    blk = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
+    if special:
+        d = SPECIAL_SCALES[rng.integers(0, SPECIAL_SCALES.size, (rows, nb))]
+    else:
+        d = f16bits(rng.uniform(scale_lo, scale_hi, (rows, nb)) * rng.choice([-1, 1], (rows, nb)))
+    blk[:, :, 0] = d & 0xFF
+    blk[:, :, 1] = d >> 8
+    return blk.reshape(rows, nb * bb)

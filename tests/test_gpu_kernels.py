@@ -1,0 +1,139 @@
+"""Kernel-level parity of the gfx950 path against the oracle (CPU restatement
+of the reference): bit-exact dequantisation, matvec and attention within
+|a-b| <= 1e-4 + 1e-3*|b| (fp32 accumulate)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.qdata import random_blocks
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 1e-4, 1e-3
+
+
+def assert_close(got, want, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bad = ~(np.abs(got - want) <= ATOL + RTOL * np.abs(want))
+    bad &= ~(np.isnan(got) & np.isnan(want))
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside tolerance; worst "
+                           f"{np.max(np.abs(got - want)[bad]):.3g}")
+
+
+@pytest.fixture(scope="module")
+def ctx(gpu):
+    c = gpu.Ctx(1 << 30)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("dtype", [2, 6, 8])
+@pytest.mark.parametrize("shape", [(16, 128), (37, 96), (64, 2048), (3, 4096)])
+def test_dequant_bit_exact(ctx, dtype, shape):
+    rows, cols = shape
+    raw = random_blocks(dtype, rows, cols, seed=rows * 7 + cols + dtype)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.dequant(t)
+    want = np.stack([O.dequant_row(raw[r], cols, dtype) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [2, 6, 8])
+def test_dequant_special_scales_bit_exact(ctx, dtype):
+    rows, cols = 48, 256
+    raw = random_blocks(dtype, rows, cols, seed=11 + dtype, special=True)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.dequant(t)
+    want = np.stack([O.dequant_row(raw[r], cols, dtype) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [2, 6, 8])
+def test_upload_concat_interleave_chunked(ctx, dtype):
+    """Row-concatenated and row-interleaved uploads, staged in small chunks,
+    dequantise to the stacked / interleaved reference rows."""
+    cols = 160
+    a = random_blocks(dtype, 40, cols, seed=1)
+    b = random_blocks(dtype, 24, cols, seed=2)
+    c = random_blocks(dtype, 24, cols, seed=3)
+    bb = a.shape[1]
+    t = ctx.qtensor([a, b, c], dtype, cols, [40, 24, 24], mode=0, staging_bytes=bb * 5)
+    want = np.concatenate([a, b, c])
+    got = ctx.dequant(t)
+    ref = np.stack([O.dequant_row(want[r], cols, dtype) for r in range(want.shape[0])])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    t2 = ctx.qtensor([b, c], dtype, cols, [24, 24], mode=1, staging_bytes=bb * 7)
+    got2 = ctx.dequant(t2)
+    il = np.empty((48, bb), np.uint8)
+    il[0::2], il[1::2] = b, c
+    ref2 = np.stack([O.dequant_row(il[r], cols, dtype) for r in range(48)])
+    assert np.array_equal(got2.view(np.uint32), ref2.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [
+    (8, 64, 256), (6, 48, 960), (2, 96, 576), (8, 49152 // 16, 576), (2, 320, 2560),
+    (2, 11008, 2048), (2, 2048, 11008), (8, 1024, 2048), (6, 2560, 960)])
+def test_gemv_matches_oracle(ctx, dtype, rows, cols):
+    raw = random_blocks(dtype, rows, cols, seed=rows + cols + dtype)
+    x = np.random.default_rng(5).standard_normal(cols).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.gemm(t, x)[0]
+    want = O.matmul(raw, x, rows, cols, dtype, O.AVX512)[:, 0]
+    assert_close(got, want, f"gemv q{dtype} {rows}x{cols}")
+
+
+def test_gemv_rmsnorm_prologue(ctx):
+    rows, cols, dtype = 256, 2048, 2
+    raw = random_blocks(dtype, rows, cols, seed=9)
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(cols) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.gemm(t, x, norm_w=w, eps=1e-6)[0]
+    xn = O.rms_norm(x, w, 1e-6)
+    want = O.matmul(raw, xn, rows, cols, dtype, O.AVX512)[:, 0]
+    assert_close(got, want, "gemv with RMSNorm prologue")
+
+
+def test_gemv_reference_kats(ctx):
+    """Reference tests/test_quant.c:272-320: Q8_0 known answers 1.0, 6.0, 11.0."""
+    def blk(d, qs):
+        b = np.zeros(34, np.uint8)
+        b[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+        for i, v in qs.items():
+            b[2 + i] = np.uint8(np.int8(v).view(np.uint8))
+        return b
+    a = np.stack([blk(1.0, {0: 1}), blk(3.0, {1: 1})])
+    x = np.zeros(32, np.float32); x[0], x[1] = 1.0, 2.0
+    t = ctx.qtensor([a], 8, 32, [2])
+    assert ctx.gemm(t, x)[0].tolist() == [1.0, 6.0]
+    a2 = np.concatenate([blk(1.0, {0: 5}), blk(2.0, {0: 3})])[None]
+    x2 = np.zeros(64, np.float32); x2[0] = x2[32] = 1.0
+    t2 = ctx.qtensor([a2], 8, 64, [1])
+    assert ctx.gemm(t2, x2)[0].tolist() == [11.0]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d_head,lens", [
+    (9, 3, 64, [1, 17, 160]), (16, 4, 128, [2304, 5, 700]), (15, 5, 64, [64, 1024]),
+    (4, 4, 128, [333])])
+def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens):
+    n = len(lens)
+    max_ctx = max(lens)
+    rng = np.random.default_rng(n_heads * 100 + d_head)
+    q = rng.standard_normal((n, n_heads * d_head)).astype(np.float32)
+    kc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
+    vc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
+    sl = np.array(lens, np.int32)
+    dq, dk, dv, ds = ctx.upload(q), ctx.upload(kc), ctx.upload(vc), ctx.upload(sl)
+    dout = ctx.alloc(q.nbytes)
+    import ctypes as C
+    gpu.check(gpu.lib().cmolhip_attn_decode(ctx.h, n, C.c_void_p(dq), C.c_void_p(dk), C.c_void_p(dv),
+                                            C.c_void_p(ds), n_heads, n_kv, d_head, max_ctx, 0,
+                                            C.c_void_p(dout)), "attn")
+    got = ctx.d2h(dout, q.shape, np.float32)
+    for i, L in enumerate(lens):
+        # oracle cache layout: [pos][n_kv][d_head]
+        kref = np.ascontiguousarray(kc[i].transpose(1, 0, 2)[:L])
+        vref = np.ascontiguousarray(vc[i].transpose(1, 0, 2)[:L])
+        want = O.attention(q[i], kref, vref, L, n_heads, n_kv, d_head)
+        assert_close(got[i], want, f"attention session {i} len {L}")
