@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""bench.py — decode throughput of libcmol's MI355X path on synthetic models.
+
+Headline (`value`): single-session greedy decode tokens/s of the
+SmolLM3-3B-shaped Q4_0 model (Q8_0 tied embedding/LM head) after a
+2048-token prompt; one step = one decode token through the whole model.
+Also reported on the same line:
+  * 32-session lock-step decode tokens/s (fp16 KV, ragged contexts drawn
+    log-uniformly from 512 to 16384, synthetic KV contents);
+  * the isolated Q4_0 matvecs 11008x2048 and 2048x11008 at batch 1 and 8 with
+    64 rotating weight copies (defeating the 256 MB Infinity Cache), timed with
+    HIP events on the stream they run on -> `roofline`;
+  * the oracle's (CPU restatement of the reference) single-thread decode of
+    the same model on a bounded sample -> `cpu_baseline`.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import libcmol_amd.native as native  # noqa: E402
+from libcmol_amd import hiprt, synth  # noqa: E402
+
+METRIC = "decode tok/s SmolLM3-3B Q4_0 (1 & 32 sessions); matvec HBM GB/s % of peak"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def q4_bytes(m, k, n):
+    return m * (k // 32) * 18 + 4 * k * n + 4 * m * n
+
+
+def bench_matvec(rows, cols, n, copies, launches):
+    """Average launch time of the Q4_0 matvec over `copies` distinct weight
+    buffers, HIP events on the context stream."""
+    w = synth.normal(rows * cols, seed=1234, stream=rows * 7 + cols, std=0.02)
+    raw = synth.quantize(synth.Q4_0, w).reshape(rows, -1)
+    tensor_bytes = native.lib().cmolhip_qtensor_bytes(2, rows, cols)
+    arena = copies * (tensor_bytes + 4096) + raw.nbytes + 64 * cols * 4 + 64 * rows * 4 + (64 << 20)
+    ctx = native.Ctx(arena)
+    stg = ctx.alloc(raw.nbytes)
+    ts = [ctx.qtensor([raw], 2, cols, [rows], staging_bytes=raw.nbytes, staging=stg)
+          for _ in range(copies)]
+    x = np.random.default_rng(1).standard_normal((n, cols)).astype(np.float32)
+    dx = ctx.upload(x)
+    dy = ctx.alloc(n * rows * 4)
+    L = native.lib()
+    for i in range(min(copies, 8)):
+        native.check(L.cmolhip_gemm(ctx.h, C.byref(ts[i]), C.c_void_p(dx), C.c_void_p(dy), n, None, 0.0))
+    native.check(L.cmolhip_synchronize(ctx.h))
+    ev = hiprt.EventTimer(ctx.stream())
+    ev.start()
+    for i in range(launches):
+        L.cmolhip_gemm(ctx.h, C.byref(ts[i % copies]), C.c_void_p(dx), C.c_void_p(dy), n, None, 0.0)
+    ev.stop()
+    ms = ev.elapsed()
+    ev.close()
+    ctx.close()
+    per_launch_s = ms / 1e3 / launches
+    b = q4_bytes(rows, cols, n)
+    return {"shape": f"{rows}x{cols}", "n": n, "us_per_launch": per_launch_s * 1e6,
+            "bytes_per_launch": b, "GBps": b / per_launch_s / 1e9,
+            "frac_of_peak": b / per_launch_s / 1e9 / HBM_PEAK_GBPS}
+
+
+def bench_decode_1(path, spec, prompt_len, steps, warmup):
+    max_ctx = prompt_len + warmup + steps + 8
+    m = native.Model(path, max_ctx=max_ctx, max_sessions=1)
+    s = m.acquire()
+    prompt = synth.tokens(prompt_len, 42, spec.vocab)
+    t0 = time.perf_counter()
+    tok, _ = s.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    pos = prompt_len
+    for _ in range(warmup):
+        tok, _ = s.forward(tok, pos)
+        pos += 1
+    stream = native.lib().cmolhip_session_stream(m.device, s.slot)
+    ev = hiprt.EventTimer(stream)
+    hiprt.device_synchronize()
+    ev.start()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok, _ = s.forward(tok, pos)
+        pos += 1
+    ev.stop()
+    hiprt.device_synchronize()
+    wall = time.perf_counter() - t0
+    dev_ms = ev.elapsed()
+    ev.close()
+    m.close()
+    return {"tok_s": steps / wall, "ms_per_step": wall * 1e3 / steps,
+            "device_ms_per_step": dev_ms / steps, "prefill_tok_s": prompt_len / prefill_s,
+            "prefill_s": prefill_s}
+
+
+def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
+    lens = synth.log_uniform_lengths(sessions, lo, hi, seed=7)
+    max_ctx = int(lens.max()) + warmup + steps + 8
+    os.environ["CMOL_KV_F16"] = "1"
+    try:
+        m = native.Model(path, max_ctx=max_ctx, max_sessions=sessions)
+    finally:
+        os.environ.pop("CMOL_KV_F16", None)
+    ss = [m.acquire() for _ in range(sessions)]
+    for i, s in enumerate(ss):
+        s.fill_kv(int(lens[i]), seed=100 + i)
+    toks = synth.tokens(sessions, 5, spec.vocab)
+    for _ in range(warmup):
+        toks = native.decode_batch(ss, toks)
+    hiprt.device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = native.decode_batch(ss, toks)
+    hiprt.device_synchronize()
+    wall = time.perf_counter() - t0
+    m.close()
+    kv_bytes = float(np.sum(lens)) * spec.n_layers * 2 * spec.n_kv_heads * spec.d_head * 2
+    return {"tok_s": sessions * steps / wall, "ms_per_step": wall * 1e3 / steps,
+            "sessions": sessions, "mean_ctx": float(np.mean(lens)),
+            "kv_bytes_per_step": kv_bytes}
+
+
+def cpu_baseline(path, spec, n_tokens):
+    """The oracle (reference arithmetic restated in C), one thread, decoding
+    n_tokens positions of the same model."""
+    from oracle import oracle as O
+    om = O.Model(path, max_ctx=n_tokens + 4, order=O.AVX512, nthreads=1)
+    toks = synth.tokens(n_tokens, 42, spec.vocab)
+    om.forward(int(toks[0]), 0)
+    t0 = time.perf_counter()
+    for p in range(1, n_tokens):
+        om.forward(int(toks[p]), p)
+    el = time.perf_counter() - t0
+    om.close()
+    return {"value": (n_tokens - 1) / el, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{n_tokens - 1} decode steps of the same SmolLM3-3B-shaped Q4_0 model "
+                      f"(single session, positions 1..{n_tokens - 1}), oracle in the reference's "
+                      f"AVX-512 accumulation order, 1 thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--sessions", type=int, default=32)
+    ap.add_argument("--multi-steps", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--skip", default="", help="comma list of: multi,matvec,cpu")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              f"(every configuration fits one MI355X; sessions shard by data parallelism)",
+              file=sys.stderr)
+        sys.exit(2)
+    skip = set(filter(None, args.skip.split(",")))
+    if native.device_count() < 1:
+        raise SystemExit("no GPU visible")
+    spec = synth.PRESETS["smollm3-3b-q4_0"]
+    t0 = time.perf_counter()
+    path = synth.model_file(spec)
+    log(f"model file ready in {time.perf_counter() - t0:.1f}s: {path}")
+
+    log("single-session decode")
+    d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup)
+    log(json.dumps(d1))
+    mv = []
+    if "matvec" not in skip:
+        for rows, cols in ((11008, 2048), (2048, 11008)):
+            for n in (1, 8):
+                r = bench_matvec(rows, cols, n, copies=64, launches=256)
+                log(json.dumps(r))
+                mv.append(r)
+    d32 = None
+    if "multi" not in skip:
+        log("32-session decode")
+        d32 = bench_decode_32(path, spec, args.sessions, args.multi_steps, 2)
+        log(json.dumps(d32))
+    cpu = None
+    if "cpu" not in skip:
+        log("cpu baseline")
+        cpu = cpu_baseline(path, spec, args.cpu_tokens)
+        log(json.dumps(cpu))
+
+    weight_bytes = spec.weight_bytes_per_token()
+    roof = None
+    if mv:
+        r = mv[0]
+        roof = {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(r["frac_of_peak"], 4), "traffic": None,
+                "kernel": "k_gemv1<Q4_0> 11008x2048 n=1",
+                "bytes_per_launch": r["bytes_per_launch"],
+                "us_per_launch": round(r["us_per_launch"], 3)}
+    out = {
+        "metric": METRIC,
+        "value": round(d1["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random weights ~N(0,0.02), seeded random prompt ids)",
+        "config": {"workload": "SmolLM3-3B-shaped Q4_0 (Q8_0 tied embd/LM head), 1 session, "
+                               f"greedy decode after a {args.prompt}-token prompt",
+                   "sessions": 1, "prompt": args.prompt,
+                   "weight_bytes_per_token": weight_bytes,
+                   "effective_weight_GBps": round(weight_bytes * d1["tok_s"] / 1e9, 1)},
+        "decode_1": d1,
+        "decode_32": d32,
+        "matvec": mv,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

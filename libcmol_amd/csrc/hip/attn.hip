@@ -6,14 +6,16 @@
 // and kv head are cut into splits of `split` positions; one work-group per
 // (kv head, split, vector) loads K/V for its split once and serves all G
 // query heads of the group.  Each split keeps (max, sum of exp, unnormalised
-// output); the last work-group of a (vector, kv head) to finish merges the
-// splits with the usual log-sum-exp rescaling and writes out.
+// output); a second kernel (k_attn_merge) combines the splits with the usual
+// log-sum-exp rescaling.  A session whose length fits one split is finished
+// directly by k_attn.
 #include "common.h"
 #include "kernels.h"
 
 #define ATT_THREADS 256
 #define ATT_MAX_G 8
 #define ATT_MAX_SPLIT 256
+#define ATT_MAX_MERGE 1024
 
 template <typename KT> struct KLoad;
 template <> struct KLoad<float> {
@@ -44,8 +46,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a)
     __shared__ float qsh[ATT_MAX_G][DH];
     __shared__ float sc[ATT_MAX_G][ATT_MAX_SPLIT];
     __shared__ float hm[ATT_MAX_G], hl[ATT_MAX_G];
-    __shared__ float red[ATT_THREADS * 4];
-    __shared__ int is_last;
+    __shared__ __attribute__((aligned(16))) float red[ATT_MAX_G * ATT_THREADS * 4];
 
     const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH;
     const KT *kb = (const KT *)a.kv.k_base + off;
@@ -103,65 +104,82 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a)
     }
     __syncthreads();
 
-    // o[h][d] = sum_p e_p V_p : DG dim groups of 4 x PG position groups
+    // o[h][d] = sum_p e_p V_p for all G heads at once: DG dim groups of 4 x
+    // PG position groups; V of each position is loaded once.
     constexpr int DG = DH / 4, PG = ATT_THREADS / DG;
     const int dg = tid % DG, pg = tid / DG;
     const size_t sbase = (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G;
-    for (int h = 0; h < G; h++) {
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int p = pg; p < cnt; p += PG) {
-            float4 v = KLoad<KT>::ld4(vb + (size_t)(t0 + p) * DH + 4 * dg);
-            float e = sc[h][p];
-            o.x = fmaf(e, v.x, o.x);
-            o.y = fmaf(e, v.y, o.y);
-            o.z = fmaf(e, v.z, o.z);
-            o.w = fmaf(e, v.w, o.w);
+    float4 o[ATT_MAX_G];
+#pragma unroll
+    for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int p = pg; p < cnt; p += PG) {
+        const float4 v = KLoad<KT>::ld4(vb + (size_t)(t0 + p) * DH + 4 * dg);
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) {
+            if (h < G) {
+                const float e = sc[h][p];
+                o[h].x = fmaf(e, v.x, o[h].x);
+                o[h].y = fmaf(e, v.y, o[h].y);
+                o[h].z = fmaf(e, v.z, o[h].z);
+                o[h].w = fmaf(e, v.w, o[h].w);
+            }
         }
-        red[(pg * DG + dg) * 4 + 0] = o.x;
-        red[(pg * DG + dg) * 4 + 1] = o.y;
-        red[(pg * DG + dg) * 4 + 2] = o.z;
-        red[(pg * DG + dg) * 4 + 3] = o.w;
-        __syncthreads();
-        for (int d = tid; d < DH; d += ATT_THREADS) {
-            float s = 0.0f;
-            for (int q = 0; q < PG; q++) s += red[q * DH + d];
-            a.po[(sbase + h) * DH + d] = s;
-        }
-        __syncthreads();
     }
+#pragma unroll
+    for (int h = 0; h < ATT_MAX_G; h++) {
+        if (h < G) *(float4 *)&red[((size_t)pg * G + h) * DH + 4 * dg] = o[h];
+    }
+    __syncthreads();
+    const bool single = nact == 1;
+    for (int i = tid; i < G * DH; i += ATT_THREADS) {
+        const int h = i / DH, d = i % DH;
+        float s = 0.0f;
+        for (int q = 0; q < PG; q++) s += red[((size_t)q * G + h) * DH + d];
+        if (single) a.out[(size_t)n * a.out_stride + (size_t)(kvh * G + h) * DH + d] = s / hl[h];
+        else a.po[(sbase + h) * DH + d] = s;
+    }
+    if (single) return;
     if (tid < G) {
         a.pm[sbase + tid] = hm[tid];
         a.pl[sbase + tid] = hl[tid];
     }
+}
 
-    // the last split of this (vector, kv head) merges all splits
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        int old = atomicAdd(&a.counters[n * a.n_kv + kvh], 1);
-        is_last = (old == nact - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
+// Merge of the splits of one (kv head, vector): M = max_s m_s,
+// L = sum_s l_s e^(m_s - M), out = sum_s o_s e^(m_s - M) / L.  Sessions whose
+// length fits one split were finished by k_attn.
+template <int DH>
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
+{
+    const int kvh = blockIdx.x, n = blockIdx.y, tid = threadIdx.x;
+    const int G = a.n_heads / a.n_kv;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int nact = (L + a.split - 1) / a.split;
+    if (nact <= 1) return;
+    __shared__ float wsh[ATT_MAX_G][ATT_MAX_MERGE];
+    __shared__ float inv_l[ATT_MAX_G];
     const size_t hb = (((size_t)n * a.n_kv + kvh) * a.max_splits) * G;
-    for (int h = 0; h < G; h++) {
+    const int w = tid >> 6, lane = tid & 63;
+    for (int h = w; h < G; h += ATT_THREADS / 64) {
         float M = -INFINITY;
-        for (int s = 0; s < nact; s++) M = fmaxf(M, __builtin_nontemporal_load(&a.pm[hb + (size_t)s * G + h]));
+        for (int s = lane; s < nact; s += 64) M = fmaxf(M, a.pm[hb + (size_t)s * G + h]);
+        M = wave_max(M);
         float Ls = 0.0f;
-        for (int s = 0; s < nact; s++)
-            Ls += __builtin_nontemporal_load(&a.pl[hb + (size_t)s * G + h]) *
-                  expf(__builtin_nontemporal_load(&a.pm[hb + (size_t)s * G + h]) - M);
-        for (int d = tid; d < DH; d += ATT_THREADS) {
-            float o = 0.0f;
-            for (int s = 0; s < nact; s++) {
-                float w = expf(__builtin_nontemporal_load(&a.pm[hb + (size_t)s * G + h]) - M);
-                o += __builtin_nontemporal_load(&a.po[(hb + (size_t)s * G + h) * DH + d]) * w;
-            }
-            a.out[(size_t)n * a.out_stride + (size_t)(kvh * G + h) * DH + d] = o / Ls;
+        for (int s = lane; s < nact; s += 64) {
+            const float e = expf(a.pm[hb + (size_t)s * G + h] - M);
+            wsh[h][s] = e;
+            Ls += a.pl[hb + (size_t)s * G + h] * e;
         }
+        Ls = wave_sum(Ls);
+        if (lane == 0) inv_l[h] = 1.0f / Ls;
     }
-    if (tid == 0) a.counters[n * a.n_kv + kvh] = 0;
+    __syncthreads();
+    for (int i = tid; i < G * DH; i += ATT_THREADS) {
+        const int h = i / DH, d = i % DH;
+        float o = 0.0f;
+        for (int s = 0; s < nact; s++) o += a.po[(hb + (size_t)s * G + h) * DH + d] * wsh[h][s];
+        a.out[(size_t)n * a.out_stride + (size_t)(kvh * G + h) * DH + d] = o * inv_l[h];
+    }
 }
 
 int attn_max_splits(int max_ctx, int split) { return (max_ctx + split - 1) / split; }
@@ -171,13 +189,18 @@ int launch_attn(const AttnArgs &a, hipStream_t s)
     const int G = a.n_heads / a.n_kv;
     if (G < 1 || G > ATT_MAX_G || a.n_heads % a.n_kv || a.split < 1 || a.split > ATT_MAX_SPLIT)
         return -4;
-    dim3 grid(a.n_kv, a.max_splits, a.n), block(ATT_THREADS);
+    if (a.max_splits > ATT_MAX_MERGE) return -4;
+    dim3 grid(a.n_kv, a.max_splits, a.n), block(ATT_THREADS), mgrid(a.n_kv, a.n);
 #define ATT(DHV)                                                                          \
     if (a.kv_f16) hipLaunchKernelGGL((k_attn<DHV, _Float16>), grid, block, 0, s, a);      \
-    else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);                  \
+    if (a.max_splits > 1) hipLaunchKernelGGL((k_attn_merge<DHV>), mgrid, block, 0, s, a);
     switch (a.d_head) {
+    case 16: ATT(16); break;
+    case 32: ATT(32); break;
     case 64: ATT(64); break;
     case 128: ATT(128); break;
+    case 256: ATT(256); break;
     default: return -4;
     }
 #undef ATT

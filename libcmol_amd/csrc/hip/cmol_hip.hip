@@ -337,16 +337,13 @@ int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kca
     int rc = E_OK;
     do {
         float *pm, *pl, *po;
-        int *cnt;
         int32_t *ids;
         const size_t np = (size_t)n * n_kv * ms * G;
         if ((rc = arena_get(c, np, &pm)) || (rc = arena_get(c, np, &pl)) ||
-            (rc = arena_get(c, np * d_head, &po)) || (rc = arena_get(c, (size_t)n * n_kv, &cnt)) ||
-            (rc = arena_get(c, (size_t)n, &ids)))
+            (rc = arena_get(c, np * d_head, &po)) || (rc = arena_get(c, (size_t)n, &ids)))
             break;
         std::vector<int32_t> hid(n);
         for (int i = 0; i < n; i++) hid[i] = i;
-        if (hipMemsetAsync(cnt, 0, (size_t)n * n_kv * 4, c->stream) != hipSuccess) { rc = E_INVALID; break; }
         if ((rc = cmolhip_memcpy_h2d(c, ids, hid.data(), (size_t)n * 4))) break;
         AttnArgs a{};
         a.q = q;
@@ -369,7 +366,6 @@ int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kca
         a.pm = pm;
         a.pl = pl;
         a.po = po;
-        a.counters = cnt;
         a.out = out;
         a.out_stride = n_heads * d_head;
         if ((rc = launch_attn(a, c->stream))) break;
@@ -400,7 +396,6 @@ struct MSlot {
     float *x = nullptr, *q = nullptr, *ao = nullptr, *h = nullptr, *logits = nullptr;
     unsigned long long *argmax = nullptr;
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
-    int *counters = nullptr;
     int32_t *h_steps = nullptr;   // pinned host [max_ctx][3]
     unsigned long long *h_argmax = nullptr;
     hipGraph_t graph = nullptr;
@@ -453,7 +448,9 @@ int validate_desc(const cmolhip_model_desc_t *d)
     if (h.d_model % 32 || h.d_ffn % 32 || h.n_heads % h.n_kv_heads ||
         h.d_head * h.n_heads != h.d_model)
         return E_UNSUPPORTED;
-    if ((h.d_head != 64 && h.d_head != 128) || h.n_heads / h.n_kv_heads > 8) return E_UNSUPPORTED;
+    if ((h.d_head != 16 && h.d_head != 32 && h.d_head != 64 && h.d_head != 128 && h.d_head != 256) ||
+        h.n_heads / h.n_kv_heads > 8)
+        return E_UNSUPPORTED;
     const int kvd = h.n_kv_heads * h.d_head;
     auto chk = [](const cmolhip_host_tensor_t &t, int rows, int cols) {
         return t.data && t.rows == rows && t.cols == cols && is_block_fmt(t.dtype);
@@ -530,11 +527,10 @@ Plan make_plan(const cmolhip_model_desc_t *d)
         P.add((size_t)h.d_model * 4);
         P.add((size_t)h.d_ffn * 4);
         P.add((size_t)h.vocab * 4);
-        P.add(8);
+        P.add(8 * ARGMAX_SLOTS);
         P.add(np * 4);
         P.add(np * 4);
         P.add(np * h.d_head * 4);
-        P.add((size_t)h.n_kv_heads * 4);
     }
     return P;
 }
@@ -613,7 +609,6 @@ int enqueue_decode(cmolhip_model *m, MSlot &S, hipStream_t st)
         at.pm = S.pm;
         at.pl = S.pl;
         at.po = S.po;
-        at.counters = S.counters;
         at.out = S.ao;
         at.out_stride = d;
         RC(launch_attn(at, st));
@@ -736,18 +731,16 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
         RC(arena_get(c, (size_t)h.d_model, &S.ao));
         RC(arena_get(c, (size_t)h.d_ffn, &S.h));
         RC(arena_get(c, (size_t)h.vocab, &S.logits));
-        RC(arena_get(c, 1, &S.argmax));
+        RC(arena_get(c, ARGMAX_SLOTS, &S.argmax));
         RC(arena_get(c, np, &S.pm));
         RC(arena_get(c, np, &S.pl));
         RC(arena_get(c, np * h.d_head, &S.po));
-        RC(arena_get(c, (size_t)h.n_kv_heads, &S.counters));
-        HC(hipMemsetAsync(S.counters, 0, (size_t)h.n_kv_heads * 4, c->stream));
         HC(hipMemsetAsync(S.step, 0, 16, c->stream));
         int32_t sid = s;
         RC(cmolhip_memcpy_h2d(c, S.slot_id, &sid, 4));
         HC(hipStreamCreateWithFlags(&S.st, hipStreamNonBlocking));
         HC(hipHostMalloc((void **)&S.h_steps, (size_t)h.max_ctx * 3 * 4, hipHostMallocDefault));
-        HC(hipHostMalloc((void **)&S.h_argmax, 8, hipHostMallocDefault));
+        HC(hipHostMalloc((void **)&S.h_argmax, 8 * ARGMAX_SLOTS, hipHostMallocDefault));
     }
     HC(hipStreamSynchronize(c->stream));
     if (m->use_graph) {
@@ -764,6 +757,13 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     return E_OK;
 }
 
+unsigned long long reduce_slots(const unsigned long long *k)
+{
+    unsigned long long best = 0;
+    for (int i = 0; i < ARGMAX_SLOTS; i++) best = k[i] > best ? k[i] : best;
+    return best;
+}
+
 int run_step(cmolhip_model *m, MSlot &S)
 {
     if (S.gexec) {
@@ -775,11 +775,11 @@ int run_step(cmolhip_model *m, MSlot &S)
 
 int finish_step(cmolhip_model *m, MSlot &S, float *logits_host, int32_t *argmax)
 {
-    HC(hipMemcpyAsync(S.h_argmax, S.argmax, 8, hipMemcpyDeviceToHost, S.st));
+    HC(hipMemcpyAsync(S.h_argmax, S.argmax, 8 * ARGMAX_SLOTS, hipMemcpyDeviceToHost, S.st));
     if (logits_host)
         HC(hipMemcpyAsync(logits_host, S.logits, (size_t)m->hp.vocab * 4, hipMemcpyDeviceToHost, S.st));
     HC(hipStreamSynchronize(S.st));
-    if (argmax) *argmax = (int32_t)argmax_index(*S.h_argmax);
+    if (argmax) *argmax = (int32_t)argmax_index(reduce_slots(S.h_argmax));
     return E_OK;
 }
 
@@ -898,7 +898,7 @@ int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const 
         hipError_t e = hipMemcpyAsync(S.step, S.h_steps, 12, hipMemcpyHostToDevice, S.st);
         int rc = e == hipSuccess ? run_step(m, S) : herr(e);
         if (rc == E_OK) {
-            e = hipMemcpyAsync(S.h_argmax, S.argmax, 8, hipMemcpyDeviceToHost, S.st);
+            e = hipMemcpyAsync(S.h_argmax, S.argmax, 8 * ARGMAX_SLOTS, hipMemcpyDeviceToHost, S.st);
             if (e == hipSuccess && logits_host)
                 e = hipMemcpyAsync(logits_host + (size_t)i * m->hp.vocab, S.logits,
                                    (size_t)m->hp.vocab * 4, hipMemcpyDeviceToHost, S.st);
@@ -916,7 +916,7 @@ int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const 
     for (int i = 0; i < n; i++) {
         MSlot &S = *m->slots[slots[i]];
         if (hipStreamSynchronize(S.st) != hipSuccess) rc = E_INVALID;
-        if (argmax) argmax[i] = (int32_t)argmax_index(*S.h_argmax);
+        if (argmax) argmax[i] = (int32_t)argmax_index(reduce_slots(S.h_argmax));
         S.mu.unlock();
     }
     return rc;

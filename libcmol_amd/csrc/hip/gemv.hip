@@ -44,36 +44,35 @@ __device__ inline void load_group(const float *__restrict__ src, int K, int gi, 
     }
 }
 
+// Block-wide (sum, max, max) of three per-thread values with one exchange.
 template <int NW>
-__device__ inline float block_sum(float v, float *stat)
+__device__ inline void block_reduce3(float &sum, float &mx0, float &mx1, float *stat)
 {
-    v = wave_sum(v);
+    sum = wave_sum(sum);
+    mx0 = wave_max(mx0);
+    mx1 = wave_max(mx1);
     const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        stat[wid] = sum;
+        stat[NW + wid] = mx0;
+        stat[2 * NW + wid] = mx1;
+    }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) stat[wid] = v;
-    __syncthreads();
-    float s = 0.0f;
+    sum = 0.0f;
+    mx0 = 0.0f;
+    mx1 = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NW; w++) s += stat[w];
-    return s;
-}
-
-template <int NW>
-__device__ inline float block_max(float v, float *stat)
-{
-    v = wave_max(v);
-    const int wid = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) stat[wid] = v;
-    __syncthreads();
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; w++) s = fmaxf(s, stat[w]);
-    return s;
+    for (int w = 0; w < NW; w++) {
+        sum += stat[w];
+        mx0 = fmaxf(mx0, stat[NW + w]);
+        mx1 = fmaxf(mx1, stat[2 * NW + w]);
+    }
 }
 
 // Stage x (optionally RMS-normalised) as f16 hi/lo into LDS:
-// xs[(b*4+g)*2 + {0:hi,1:lo}] = 8 halves.  Returns 1/scale.
+// xs[(b*4+g)*2 + {0:hi,1:lo}] = 8 halves.  Returns 1/scale.  Pass 1 gathers
+// the statistics, pass 2 re-reads x (cache-resident) to keep registers free
+// for the weight prefetch that is in flight meanwhile.
 template <int DT, int NW>
 __device__ float stage_single(const GemvArgs &a, const float *__restrict__ x,
                               uint8_t *xs, float *stat)
@@ -87,7 +86,10 @@ __device__ float stage_single(const GemvArgs &a, const float *__restrict__ x,
         float v[8];
         load_group<DT>(x, K, gi, v);
 #pragma unroll
-        for (int e = 0; e < 8; e++) { ss += v[e] * v[e]; mx = fmaxf(mx, fabsf(v[e])); }
+        for (int e = 0; e < 8; e++) {
+            ss += v[e] * v[e];
+            mx = fmaxf(mx, fabsf(v[e]));
+        }
         if (norm) {
             float w[8];
             load_group<DT>(a.norm_w, K, gi, w);
@@ -95,14 +97,9 @@ __device__ float stage_single(const GemvArgs &a, const float *__restrict__ x,
             for (int e = 0; e < 8; e++) wm = fmaxf(wm, fabsf(w[e]));
         }
     }
-    float s = 1.0f;
-    if (norm) {
-        ss = block_sum<NW>(ss, stat);
-        wm = block_max<NW>(wm, stat);
-        s = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
-    mx = block_max<NW>(mx, stat);
-    float bound = norm ? mx * s * wm : mx;
+    block_reduce3<NW>(ss, mx, wm, stat);
+    const float s = norm ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
+    const float bound = norm ? mx * s * wm : mx;
     float scale = 1.0f, inv = 1.0f;
     if (bound > 0.0f && bound < 3.0e38f) {
         int E;
@@ -117,9 +114,9 @@ __device__ float stage_single(const GemvArgs &a, const float *__restrict__ x,
         f16x8 hi, lo;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            float xn = norm ? w[e] * (v[e] * s) : v[e];
-            float t = xn * scale;
-            _Float16 h = (_Float16)t;
+            const float xn = norm ? w[e] * (v[e] * s) : v[e];
+            const float t = xn * scale;
+            const _Float16 h = (_Float16)t;
             hi[e] = h;
             lo[e] = (_Float16)(t - (float)h);
         }
@@ -186,7 +183,7 @@ __device__ void epilogue(const GemvArgs &a, int t, int l, float y)
             unsigned long long other = __shfl_xor(key, o, 64);
             key = other > key ? other : key;
         }
-        if (l == 0) atomicMax(a.argmax, key);
+        if (l == 0) atomicMax(a.argmax + (t & (ARGMAX_SLOTS - 1)), key);
     }
 }
 
@@ -194,7 +191,7 @@ template <int DT, int NW, int EPI>
 __global__ __launch_bounds__(NW * 64) void k_gemv1(GemvArgs a)
 {
     constexpr int LB = QFmt<DT>::LANE_BYTES;
-    constexpr int U = 4;
+    constexpr int U = 8;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int BQ = a.w.block_quads;
     const int t = blockIdx.x;
@@ -206,17 +203,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemv1(GemvArgs a)
     float *red = (float *)(smem + (size_t)BQ * 512);
     float *stat = red + NW * 32;
 
-    const float inv_scale = stage_single<DT, NW>(a, a.x, xs, stat);
-
     const size_t cell0 = (size_t)t * BQ;
-    const bool holds_x = (l & 15) < 2;
-    const f16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    float acc0 = 0.0f, acc1 = 0.0f;
-    for (int qb = q0; qb < q1; qb += U) {
-        u32x4 c0[U], c1[U];
-        u32x2 dv[U];
-        uint32_t hv[U];
+    u32x4 c0[U], c1[U];
+    u32x2 dv[U];
+    uint32_t hv[U];
+    // Weights do not depend on x: issue the first batch before the prologue
+    // so its HBM latency overlaps the RMSNorm/staging work.
+    auto load_batch = [&](int qb) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const size_t cell = cell0 + (qb + u < q1 ? qb + u : qb);
@@ -228,6 +221,17 @@ __global__ __launch_bounds__(NW * 64) void k_gemv1(GemvArgs a)
             if constexpr (DT == DT_Q5_0) hv[u] = a.w.qh[cell * 64 + l];
             else hv[u] = 0u;
         }
+    };
+    if (q0 < q1) load_batch(q0);
+
+    const float inv_scale = stage_single<DT, NW>(a, a.x, xs, stat);
+
+    const bool holds_x = (l & 15) < 2;
+    const f16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int qb = q0; qb < q1; qb += U) {
+        if (qb != q0) load_batch(qb);
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (qb + u < q1) {
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv1(GemvArgs a)
 
 static int pick_nw(int tiles, int quads)
 {
-    int nw = tiles < 256 ? 16 : tiles < 1024 ? 8 : 4;
+    int nw = tiles < 1024 ? 8 : 4;
     while (nw > 4 && nw > quads) nw >>= 1;
     return nw;
 }
@@ -290,12 +294,11 @@ static void launch_dt(const GemvArgs &a, int epi, hipStream_t s)
 {
     const int nw = pick_nw(a.w.row_tiles, a.w.block_quads);
     const size_t lds = (size_t)a.w.block_quads * 512 + (size_t)nw * 32 * 4 + 64 * 4;
-    if (nw == 16) launch_dt_nw<DT, 16>(a, epi, lds, s);
-    else if (nw == 8) launch_dt_nw<DT, 8>(a, epi, lds, s);
+    if (nw == 8) launch_dt_nw<DT, 8>(a, epi, lds, s);
     else launch_dt_nw<DT, 4>(a, epi, lds, s);
 }
 
-size_t gemv_lds_bytes(int block_quads) { return (size_t)block_quads * 512 + 16 * 32 * 4 + 64 * 4; }
+size_t gemv_lds_bytes(int block_quads) { return (size_t)block_quads * 512 + 8 * 32 * 4 + 64 * 4; }
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s)
 {

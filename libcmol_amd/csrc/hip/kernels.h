@@ -37,6 +37,10 @@ int launch_embed(const QTensor &t, const int32_t *token, int token_stride, float
                  int x_stride, unsigned long long *argmax, int n, hipStream_t s);
 
 // ---- gemv.hip
+// The LM-head argmax of one vector is spread over this many 64-bit slots
+// (work-group t uses slot t % ARGMAX_SLOTS); the host reduces the slots.
+#define ARGMAX_SLOTS 64
+
 enum GemvEpilogue {
     EPI_STORE = 0,   // out[n][row] = y
     EPI_RESID = 1,   // out[n][row] += y
@@ -61,7 +65,7 @@ struct GemvArgs {
     const int32_t *pos;     // per-vector position, pos[n * pos_stride]
     int pos_stride;
     // EPI_LOGITS
-    unsigned long long *argmax;   // per session
+    unsigned long long *argmax;   // ARGMAX_SLOTS slots per vector
 };
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);
@@ -77,7 +81,6 @@ struct AttnArgs {
     int split;              // positions per work-group
     int max_splits;
     float *pm, *pl, *po;    // partials [n][n_kv][max_splits][G]( [d_head])
-    int *counters;          // [n][n_kv], zero between launches
     float *out;             // [n][out_stride]
     int out_stride;
 };

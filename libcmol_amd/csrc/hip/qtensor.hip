@@ -203,8 +203,8 @@ int launch_dequant(const QTensor &t, float *out, hipStream_t s)
 }
 
 // Embedding rows for n vectors: x[s][:] = dequant(row token[s]).  Thread per
-// block.  Also clears each vector's argmax slot for the LM head that ends the
-// step.
+// block.  Also clears each vector's argmax slots for the LM head that ends
+// the step.
 template <int DT>
 __global__ void k_embed(QTensor t, const int32_t *__restrict__ token, int token_stride,
                         float *__restrict__ x, int x_stride,
@@ -214,7 +214,8 @@ __global__ void k_embed(QTensor t, const int32_t *__restrict__ token, int token_
     if (s >= n) return;
     int nb = t.cols / 32;
     int tok = token[s * token_stride];
-    if (threadIdx.x == 0 && blockIdx.x == 0) argmax[s] = 0ull;
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < ARGMAX_SLOTS; i += blockDim.x) argmax[(size_t)s * ARGMAX_SLOTS + i] = 0ull;
     if (tok < 0 || tok >= t.rows) tok = 0;
     for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += gridDim.x * blockDim.x)
         block_values<DT>(t, tok, b, x + (size_t)s * x_stride + (size_t)b * 32, 1);

@@ -188,10 +188,10 @@ class Ctx:
         return d
 
     def qtensor(self, raw_parts, dtype: int, cols: int, rows, mode: int = 0,
-                staging_bytes: int | None = None) -> QTensor:
+                staging_bytes: int | None = None, staging: int | None = None) -> QTensor:
         parts = [np.ascontiguousarray(p, np.uint8) for p in raw_parts]
         staging_bytes = staging_bytes or max(p.nbytes for p in parts)
-        stg = self.alloc(staging_bytes)
+        stg = staging if staging is not None else self.alloc(staging_bytes)
         arr_p = (C.c_void_p * len(parts))(*[p.ctypes.data for p in parts])
         arr_r = (I32 * len(parts))(*rows)
         t = QTensor()
