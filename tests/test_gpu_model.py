@@ -1,5 +1,8 @@
 """Whole-model decode on the GPU against the oracle: identical greedy token
 ids, logits within 1e-3 relative / 1e-4 absolute."""
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -12,6 +15,31 @@ pytestmark = pytest.mark.gpu
 
 def close_frac(got, want, atol=1e-4, rtol=1e-3):
     return np.mean(np.abs(got - want) <= atol + rtol * np.abs(want))
+
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+G = np.load(os.path.join(HERE, "golden", "golden.npz"))
+META = json.load(open(os.path.join(HERE, "golden", "golden.json")))
+
+
+@pytest.mark.parametrize("name", sorted(META["models"]))
+def test_matches_reference_golden(gpu, model_dir, name):
+    """GPU greedy ids equal the reference's own ids (golden fixtures written by
+    the reference library), and the logits after the prompt are within
+    1e-4 + 1e-3*|ref| of the reference's."""
+    info = META["models"][name]
+    spec = synth.PRESETS[info["preset"]].replace(**info["overrides"])
+    path = synth.model_file(spec, model_dir)
+    prompt = G[f"model_{name}_prompt"]
+    m = native.Model(path, max_ctx=info["max_ctx"], max_sessions=1)
+    s = m.acquire()
+    got = s.generate_ids(prompt, native.greedy_params(info["n_new"]), info["n_new"])
+    assert got.tolist() == G[f"model_{name}_tokens"].tolist()
+    s.reset()
+    _, lg = s.prefill(prompt, spec.vocab)
+    want = G[f"model_{name}_last_prompt_logits"].view(np.float32)
+    assert close_frac(lg, want) == 1.0
+    m.close()
 
 
 @pytest.mark.parametrize("preset", ["micro-q8_0", "micro-q4_0", "micro-q5_0", "small-q4_0",
@@ -83,4 +111,12 @@ def test_smollm2_135m_greedy_128(gpu, model_dir):
     want, margins = om.generate(prompt, 128, margins=True)
     print("min top-2 margin over 128 steps:", float(margins.min()))
     assert got[:64].tolist() == want[:64].tolist()
+    assert got.tolist() == G["smollm2_135m_tokens"].tolist()   # the reference's ids
+    # logits of the last prompt position
+    s.reset()
+    _, lg = s.prefill(prompt, spec.vocab)
+    om2 = O.Model(path, 256)
+    for p, t in enumerate(prompt):
+        ref = om2.forward(int(t), p)
+    assert close_frac(lg, ref) == 1.0
     m.close()

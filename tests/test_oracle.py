@@ -1,0 +1,240 @@
+"""The oracle (CPU restatement of the reference) against the reference's own
+outputs (golden fixtures written by tests/golden/make_golden.py from the
+reference built from its sources), the reference's own unit-test known
+answers, and properties fixed by the mathematics."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from libcmol_amd import synth
+from oracle import oracle as O
+from tests.qdata import random_blocks
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+G = np.load(os.path.join(HERE, "golden", "golden.npz"))
+META = json.load(open(os.path.join(HERE, "golden", "golden.json")))
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+# ---- fp16 -------------------------------------------------------------------
+def test_f16_table_matches_reference():
+    h = np.arange(65536, dtype=np.uint16)
+    f = O.dequant_row(h, 65536, 1)
+    assert hashlib.sha256(f.view(np.uint32).tobytes()).hexdigest() == META["f16_table_sha256"]
+    assert np.array_equal(bits(f[G["f16_special_in"].astype(np.int64)]), G["f16_special_out"])
+
+
+def test_f16_matches_numpy_for_all_non_nan():
+    """numpy's half->float conversion is an independent implementation."""
+    h = np.arange(65536, dtype=np.uint16)
+    f = O.dequant_row(h, 65536, 1)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(bits(f[~nan]), bits(ref[~nan]))
+    # NaN payload: mantissa << 13 under an all-ones exponent, sign kept
+    exp_bits = (h[nan].astype(np.uint32) & 0x8000) << 16 | 0x7F800000 | \
+        ((h[nan].astype(np.uint32) & 0x3FF) << 13)
+    assert np.array_equal(bits(f[nan]), exp_bits)
+
+
+# ---- dequantisation -----------------------------------------------------------
+@pytest.mark.parametrize("name,dt", [("q8_0", 8), ("q5_0", 6), ("q4_0", 2)])
+@pytest.mark.parametrize("tag", ["rand", "special"])
+def test_dequant_matches_reference(name, dt, tag):
+    raw = G[f"deq_{name}_{tag}_in"]
+    want = G[f"deq_{name}_{tag}_out"]
+    got = np.stack([O.dequant_row(raw[r], 128, dt) for r in range(raw.shape[0])])
+    assert np.array_equal(bits(got), want)
+
+
+def test_dequant_q8_0_reference_kats():
+    """Reference tests/test_quant.c:97-127."""
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(2.0).tobytes(), np.uint8)
+    b[2], b[3] = 3, np.uint8(np.int8(-1).view(np.uint8))
+    out = O.dequant_row(b, 32, 8)
+    assert out[0] == 6.0 and out[1] == -2.0 and out[2] == 0.0 and out[31] == 0.0
+    b2 = np.zeros(68, np.uint8)
+    b2[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8); b2[2] = 7
+    b2[34:36] = np.frombuffer(np.float16(3.0).tobytes(), np.uint8); b2[36] = 2
+    out2 = O.dequant_row(b2, 64, 8)
+    assert out2[0] == 7.0 and out2[32] == 6.0
+
+
+def test_dequant_edge_cases_are_noops():
+    """Reference tests/test_quant.c:366-386: NULL src, n=0, unknown dtype."""
+    dst = np.full(32, 9.9, np.float32)
+    blk = np.zeros(34, np.uint8)
+    O.lib().o_dequant_row(None, dst.ctypes.data, 32, 8)
+    O.lib().o_dequant_row(blk.ctypes.data, dst.ctypes.data, 0, 8)
+    O.lib().o_dequant_row(blk.ctypes.data, dst.ctypes.data, 32, 99)
+    assert np.all(dst == np.float32(9.9))
+
+
+def test_q4_0_closed_form():
+    """Q4_0 value = fp16 scale * (nibble - 8); nibble j of block is the low
+    half of byte j (j < 16) or the high half of byte j-16."""
+    raw = random_blocks(2, 8, 256, seed=3)
+    blk = raw.reshape(8, 8, 18)
+    d = blk[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    q = np.concatenate([(blk[:, :, 2:] & 0xF), (blk[:, :, 2:] >> 4)], axis=2).astype(np.float32) - 8
+    want = (d[..., None] * q).reshape(8, 256)
+    got = np.stack([O.dequant_row(raw[r], 256, 2) for r in range(8)])
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_q5_0_closed_form():
+    raw = random_blocks(6, 4, 128, seed=4)
+    blk = raw.reshape(4, 4, 22)
+    d = blk[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    qh = blk[:, :, 2:6].copy().view(np.uint32)[..., 0]
+    j = np.arange(16)
+    lo = (blk[:, :, 6:] & 0xF) | (((qh[..., None] >> j) & 1) << 4)
+    hi = (blk[:, :, 6:] >> 4) | (((qh[..., None] >> (j + 16)) & 1) << 4)
+    q = np.concatenate([lo, hi], axis=2).astype(np.float32) - 16
+    want = (d[..., None] * q).reshape(4, 128)
+    got = np.stack([O.dequant_row(raw[r], 128, 6) for r in range(4)])
+    assert np.array_equal(bits(got), bits(want))
+
+
+# ---- matmul -------------------------------------------------------------------
+@pytest.mark.parametrize("name,dt", [("q8_0", 8), ("q5_0", 6), ("q4_0", 2)])
+@pytest.mark.parametrize("shape", [(16, 128, 1), (33, 256, 1), (8, 64, 3)])
+def test_matmul_matches_reference_orders(name, dt, shape):
+    m, k, n = shape
+    key = f"mm_{name}_{m}x{k}x{n}"
+    a, b = G[key + "_a"], G[key + "_b"]
+    for order, suffix in ((O.SCALAR, "_scalar"), (O.AVX512, "_avx512")):
+        got = O.matmul(a, b, m, k, dt, order)
+        assert np.array_equal(bits(got), G[key + suffix]), suffix
+
+
+def test_matmul_f32_with_tail_matches_reference():
+    a, b = G["mm_f32_5x37x2_a"], G["mm_f32_5x37x2_b"]
+    for order, suffix in ((O.SCALAR, "_scalar"), (O.AVX512, "_avx512")):
+        assert np.array_equal(bits(O.matmul(a.view(np.uint8), b, 5, 37, 0, order)),
+                              G["mm_f32_5x37x2" + suffix])
+
+
+def test_matmul_reference_kats():
+    """Reference tests/test_quant.c:217-320."""
+    A = np.array([[1, 0, 0, 0], [0, 1, 0, 0], [1, 1, 0, 0]], np.float32)
+    assert O.matmul(A.view(np.uint8), np.array([5, 7, 0, 0], np.float32), 3, 4, 0)[:, 0].tolist() == [5, 7, 12]
+    A2 = np.array([[1, 0, 0, 0], [0, 1, 0, 0]], np.float32)
+    B2 = np.array([[1, 2], [3, 4], [0, 0], [0, 0]], np.float32)
+    assert O.matmul(A2.view(np.uint8), B2, 2, 4, 0).tolist() == [[1, 2], [3, 4]]
+    def blk(d, qs):
+        b = np.zeros(34, np.uint8)
+        b[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+        for i, v in qs.items():
+            b[2 + i] = np.uint8(np.int8(v).view(np.uint8))
+        return b
+    x = np.zeros(32, np.float32); x[0], x[1] = 1, 2
+    assert O.matmul(np.stack([blk(1, {0: 1}), blk(3, {1: 1})]), x, 2, 32, 8)[:, 0].tolist() == [1, 6]
+    x2 = np.zeros(64, np.float32); x2[0] = x2[32] = 1
+    assert O.matmul(np.concatenate([blk(1, {0: 5}), blk(2, {0: 3})]), x2, 1, 64, 8)[0, 0] == 11
+
+
+def test_matmul_matches_float64_dot():
+    """Independent: float64 dot of the dequantised rows, within fp32 rounding."""
+    raw = random_blocks(2, 64, 2048, seed=5)
+    x = np.random.default_rng(1).standard_normal(2048).astype(np.float32)
+    w = np.stack([O.dequant_row(raw[r], 2048, 2) for r in range(64)]).astype(np.float64)
+    want = w @ x.astype(np.float64)
+    for order in (O.SCALAR, O.AVX512):
+        got = O.matmul(raw, x, 64, 2048, 2, order)[:, 0]
+        assert np.allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+# ---- primitives -----------------------------------------------------------------
+def test_primitives_match_reference():
+    assert np.array_equal(bits(O.rms_norm(G["rms_x"], G["rms_w"], 1e-5)), G["rms_out"])
+    assert np.array_equal(bits(O.softmax(G["softmax_in"])), G["softmax_out"])
+    assert np.array_equal(bits(O.swiglu(G["swiglu_g"], G["swiglu_u"])), G["swiglu_out"])
+    for pos in (0, 1, 37, 2047):
+        q, k = O.rope(G[f"rope_{pos}_q"], G[f"rope_{pos}_k"], pos, 16, 4, 128, 5e6)
+        assert np.array_equal(bits(q), G[f"rope_{pos}_qo"])
+        assert np.array_equal(bits(k), G[f"rope_{pos}_ko"])
+
+
+def test_primitive_reference_kats():
+    """Reference tests/test_model.c:45-166."""
+    o = O.rms_norm(np.array([3, 4], np.float32), np.ones(2, np.float32), 0.0)
+    assert abs(o[0] - 3 / np.sqrt(12.5)) < 1e-4 and abs(o[1] - 4 / np.sqrt(12.5)) < 1e-4
+    s = O.softmax(np.array([1, 2, 3], np.float32))
+    assert abs(s.sum() - 1) < 1e-6 and s[2] > s[1] > s[0]
+    assert np.allclose(O.softmax(np.full(4, 5.0)), 0.25)
+    g = O.swiglu(np.array([0, 1], np.float32), np.array([3, 2], np.float32))
+    assert g[0] == 0 and abs(g[1] - 2 / (1 + np.exp(-1))) < 1e-3
+    q, k = O.rope(np.array([1, 2, 3, 4], np.float32), np.array([1, 2, 3, 4], np.float32), 1, 1, 1, 4, 10000.0)
+    assert abs(q[0] - (np.cos(1) - 2 * np.sin(1))) < 1e-3 and abs(q[1] - (np.sin(1) + 2 * np.cos(1))) < 1e-3
+    q0, _ = O.rope(np.arange(8, dtype=np.float32), np.arange(4, dtype=np.float32), 0, 2, 1, 4, 10000.0)
+    assert np.array_equal(q0, np.arange(8, dtype=np.float32))
+
+
+def test_rope_is_a_rotation_of_adjacent_pairs():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal(128).astype(np.float32)
+    k = rng.standard_normal(128).astype(np.float32)
+    qo, _ = O.rope(q, k, 123, 1, 1, 128, 10000.0)
+    nb = np.hypot(q[0::2], q[1::2]); na = np.hypot(qo[0::2], qo[1::2])
+    assert np.allclose(na, nb, rtol=1e-5)
+    # angle of pair i is pos / base^(2i/d) (adjacent pairs, not split halves)
+    ang = np.arctan2(qo[1::2], qo[0::2]) - np.arctan2(q[1::2], q[0::2])
+    theta = 123 / 10000.0 ** (np.arange(64) * 2 / 128)
+    d = np.angle(np.exp(1j * (ang - theta)))
+    assert np.max(np.abs(d)) < 1e-3
+
+
+def test_attention_matches_float64_bruteforce():
+    rng = np.random.default_rng(9)
+    nh, nkv, dh, L = 6, 2, 16, 13
+    q = rng.standard_normal(nh * dh).astype(np.float32)
+    kc = rng.standard_normal((L, nkv, dh)).astype(np.float32)
+    vc = rng.standard_normal((L, nkv, dh)).astype(np.float32)
+    got = O.attention(q, kc, vc, L, nh, nkv, dh)
+    want = np.zeros(nh * dh)
+    for h in range(nh):
+        hk = h * nkv // nh
+        s = kc[:, hk, :].astype(np.float64) @ q[h * dh:(h + 1) * dh].astype(np.float64) / np.sqrt(dh)
+        p = np.exp(s - s.max()); p /= p.sum()
+        want[h * dh:(h + 1) * dh] = p @ vc[:, hk, :].astype(np.float64)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+# ---- whole model -------------------------------------------------------------------
+MODEL_CASES = META["models"]
+
+
+@pytest.mark.parametrize("name", sorted(MODEL_CASES))
+def test_model_matches_reference(name, model_dir):
+    info = MODEL_CASES[name]
+    spec = synth.PRESETS[info["preset"]].replace(**info["overrides"])
+    path = synth.model_file(spec, model_dir)
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == info["sha256"]
+    prompt = G[f"model_{name}_prompt"]
+    om = O.Model(path, info["max_ctx"])
+    toks = om.generate(prompt, info["n_new"])
+    assert toks.tolist() == G[f"model_{name}_tokens"].tolist()
+    om.close()
+    om = O.Model(path, info["max_ctx"])
+    for p, t in enumerate(prompt):
+        lg = om.forward(int(t), p)
+    assert np.array_equal(bits(lg), G[f"model_{name}_last_prompt_logits"])
+    om.close()
+
+
+def test_smollm2_135m_matches_reference(model_dir):
+    spec = synth.PRESETS["smollm2-135m-q8_0"]
+    path = synth.model_file(spec, model_dir)
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == META["smollm2_135m_sha256"]
+    om = O.Model(path, 256)
+    toks = om.generate(G["smollm2_135m_prompt"], 128)
+    assert toks.tolist() == G["smollm2_135m_tokens"].tolist()
+    om.close()
