@@ -45,8 +45,11 @@ void *cmolhip_stream(cmolhip_ctx_t *c);
 
 /* ---- quantised weights in the device layout -----------------------------
  * GGUF block formats Q4_0 (2), Q5_0 (6) and Q8_0 (8) are repacked at upload
- * into 16-row x 4-block tiles matched to the gfx950 MFMA operand layout
- * (bit-preserving: codes and fp16 scales are moved, never re-quantised). */
+ * into tiles of 16 MFMA columns x 4 blocks matched to the gfx950 MFMA
+ * operand layout (bit-preserving: codes and fp16 scales are moved, never
+ * re-quantised).  With fold F (1, 2, 4 or 8) a tile holds 16/F rows and the
+ * k range is cut into F parts that share the tile's 16 columns, so narrow
+ * matrices still spread over every compute unit at batch 1. */
 typedef struct {
     void   *qs;          /* packed codes                                  */
     void   *d;           /* fp16 scales                                   */
@@ -54,13 +57,17 @@ typedef struct {
     int32_t dtype;       /* GGUF dtype id                                 */
     int32_t rows;        /* output features                               */
     int32_t cols;        /* input features (multiple of 32)               */
-    int32_t row_tiles;   /* ceil(rows / 16)                               */
-    int32_t block_quads; /* ceil(cols / 128)                              */
-    int32_t pad_;
+    int32_t row_tiles;   /* ceil(rows / (16 / fold))                      */
+    int32_t block_quads; /* block quads per k part                        */
+    int32_t fold;        /* k parts per tile: 1, 2, 4 or 8                */
 } cmolhip_qtensor_t;
 
-/* Device bytes a tensor needs (0 when dtype/shape is unsupported). */
-size_t cmolhip_qtensor_bytes(int dtype, int rows, int cols);
+/* Device bytes a tensor needs (0 when dtype/shape/fold is unsupported). */
+size_t cmolhip_qtensor_bytes(int dtype, int rows, int cols, int fold);
+
+/* The fold cmolhip_model_create gives a rows x cols projection of a model
+ * with max_sessions sessions (1 for models serving several sessions). */
+int cmolhip_pick_fold(int rows, int cols, int max_sessions);
 
 #define CMOLHIP_PARTS_CONCAT     0 /* parts stacked row-wise              */
 #define CMOLHIP_PARTS_INTERLEAVE 1 /* two parts, rows alternate p0,p1,... */
@@ -68,7 +75,7 @@ size_t cmolhip_qtensor_bytes(int dtype, int rows, int cols);
 /* Upload raw GGUF rows (host memory) of `n_parts` tensors sharing dtype and
  * cols into one device tensor.  `staging` is device scratch of at least
  * staging_bytes >= largest part's raw size. */
-int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int n_parts,
+int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int fold, int n_parts,
                            const void *const *parts, const int32_t *part_rows,
                            int mode, void *staging, size_t staging_bytes,
                            cmolhip_qtensor_t *out);
@@ -82,6 +89,18 @@ int cmolhip_dequant(cmolhip_ctx_t *c, const cmolhip_qtensor_t *t, float *dout);
  * epsilon eps).  n in 1..32.  Device pointers; runs on the context stream. */
 int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx,
                  float *dy, int n, const float *norm_w, float eps);
+
+/* The same product in two steps, for callers that reuse one activation
+ * operand: cmolhip_act_prepare converts dx[n][cols] (optionally keeping
+ * per-32-input sums of squares for an RMSNorm with weights norm_w) into the
+ * device operand `op` of cmolhip_act_bytes(cols, n) bytes for weights of
+ * dtype `dtype`; cmolhip_gemm_prepared runs the matvec on it (ss as written
+ * by the prepare step, or NULL without norm). */
+size_t cmolhip_act_bytes(int cols, int n);
+int cmolhip_act_prepare(cmolhip_ctx_t *c, const float *dx, int n, int cols, int dtype,
+                        const float *norm_w, void *op, float *ss);
+int cmolhip_gemm_prepared(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op, int n,
+                          const float *ss, float eps, float *dy);
 
 /* Reference kernel seam replacement (cmol_matmul_fn_t semantics on host
  * memory): out[m][n] = A[m][k] . B[k][n], A raw GGUF rows.  Uses the

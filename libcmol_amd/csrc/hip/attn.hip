@@ -135,8 +135,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a)
         const int h = i / DH, d = i % DH;
         float s = 0.0f;
         for (int q = 0; q < PG; q++) s += red[((size_t)q * G + h) * DH + d];
-        if (single) a.out[(size_t)n * a.out_stride + (size_t)(kvh * G + h) * DH + d] = s / hl[h];
-        else a.po[(sbase + h) * DH + d] = s;
+        if (single) {
+            const float o = s / hl[h];
+            const int k = (kvh * G + h) * DH + d;
+            if (a.out) a.out[(size_t)n * a.out_stride + k] = o;
+            if (a.next.q) act_put(a.next, n, k, o);
+        } else {
+            a.po[(sbase + h) * DH + d] = s;
+        }
     }
     if (single) return;
     if (tid < G) {
@@ -178,7 +184,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
         const int h = i / DH, d = i % DH;
         float o = 0.0f;
         for (int s = 0; s < nact; s++) o += a.po[(hb + (size_t)s * G + h) * DH + d] * wsh[h][s];
-        a.out[(size_t)n * a.out_stride + (size_t)(kvh * G + h) * DH + d] = o * inv_l[h];
+        const int k = (kvh * G + h) * DH + d;
+        if (a.out) a.out[(size_t)n * a.out_stride + k] = o * inv_l[h];
+        if (a.next.q) act_put(a.next, n, k, o * inv_l[h]);
     }
 }
 

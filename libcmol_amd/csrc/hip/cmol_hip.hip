@@ -8,6 +8,7 @@
 
 #include <cstdint>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -54,12 +55,13 @@ struct QLayout {
     int rt, bq;
 };
 
-bool qlayout(int dtype, int rows, int cols, QLayout *L)
+bool qlayout(int dtype, int rows, int cols, int fold, QLayout *L)
 {
     if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0) return false;
-    if (rows <= 0 || cols <= 0 || cols % 32) return false;
-    L->rt = (rows + 15) / 16;
-    L->bq = (cols / 32 + 3) / 4;
+    if (rows <= 0 || cols <= 0 || cols % 32 || !fold_ok(fold)) return false;
+    const int R = 16 / fold;
+    L->rt = (rows + R - 1) / R;
+    L->bq = fold_quads(cols / 32, fold);
     size_t cells = (size_t)L->rt * L->bq;
     L->qs = cells * 64 * lane_bytes_of(dtype);
     L->d = cells * 64 * 2;
@@ -67,10 +69,10 @@ bool qlayout(int dtype, int rows, int cols, QLayout *L)
     return true;
 }
 
-size_t qbytes_aligned(int dtype, int rows, int cols)
+size_t qbytes_aligned(int dtype, int rows, int cols, int fold)
 {
     QLayout L;
-    if (!qlayout(dtype, rows, cols, &L)) return 0;
+    if (!qlayout(dtype, rows, cols, fold, &L)) return 0;
     return align_up(L.qs, ALIGN) + align_up(L.d, ALIGN) + align_up(L.qh, ALIGN);
 }
 
@@ -85,6 +87,7 @@ QTensor to_qt(const cmolhip_qtensor_t &t)
     q.cols = t.cols;
     q.row_tiles = t.row_tiles;
     q.block_quads = t.block_quads;
+    q.fold = t.fold;
     return q;
 }
 
@@ -146,7 +149,7 @@ int cmolhip_ctx_create(int device, size_t bytes, cmolhip_ctx_t **out)
     if (bytes) {
         if (hipMalloc((void **)&c->arena, bytes) != hipSuccess) {
             (void)hipGetLastError();
-            hipStreamDestroy(c->stream);
+            (void)hipStreamDestroy(c->stream);
             delete c;
             return E_OOM;
         }
@@ -159,12 +162,12 @@ int cmolhip_ctx_create(int device, size_t bytes, cmolhip_ctx_t **out)
 void cmolhip_ctx_destroy(cmolhip_ctx_t *c)
 {
     if (!c) return;
-    hipSetDevice(c->device);
+    (void)hipSetDevice(c->device);
     if (c->stream) {
-        hipStreamSynchronize(c->stream);
-        hipStreamDestroy(c->stream);
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamDestroy(c->stream);
     }
-    if (c->arena) hipFree(c->arena);
+    if (c->arena) (void)hipFree(c->arena);
     delete c;
 }
 
@@ -215,9 +218,12 @@ int cmolhip_synchronize(cmolhip_ctx_t *c)
 
 void *cmolhip_stream(cmolhip_ctx_t *c) { return c ? (void *)c->stream : nullptr; }
 
-size_t cmolhip_qtensor_bytes(int dtype, int rows, int cols) { return qbytes_aligned(dtype, rows, cols); }
+size_t cmolhip_qtensor_bytes(int dtype, int rows, int cols, int fold)
+{
+    return qbytes_aligned(dtype, rows, cols, fold);
+}
 
-int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int n_parts,
+int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int fold, int n_parts,
                            const void *const *parts, const int32_t *part_rows, int mode,
                            void *staging, size_t staging_bytes, cmolhip_qtensor_t *out)
 {
@@ -232,7 +238,7 @@ int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int n_parts,
     }
     if (rows > (1L << 30)) return E_ARGS;
     QLayout L;
-    if (!qlayout(dtype, (int)rows, cols, &L)) return E_UNSUPPORTED;
+    if (!qlayout(dtype, (int)rows, cols, fold, &L)) return E_UNSUPPORTED;
     cmolhip_qtensor_t t{};
     RC(cmolhip_alloc(c, L.qs, ALIGN, &t.qs));
     RC(cmolhip_alloc(c, L.d, ALIGN, &t.d));
@@ -242,6 +248,7 @@ int cmolhip_qtensor_upload(cmolhip_ctx_t *c, int dtype, int cols, int n_parts,
     t.cols = cols;
     t.row_tiles = L.rt;
     t.block_quads = L.bq;
+    t.fold = fold;
     HC(hipMemsetAsync(t.qs, 0, L.qs, c->stream));
     HC(hipMemsetAsync(t.d, 0, L.d, c->stream));
     if (L.qh) HC(hipMemsetAsync(t.qh, 0, L.qh, c->stream));
@@ -273,30 +280,64 @@ int cmolhip_dequant(cmolhip_ctx_t *c, const cmolhip_qtensor_t *t, float *dout)
     return E_OK;
 }
 
+size_t cmolhip_act_bytes(int cols, int n) { return (cols > 0 && n > 0) ? act_bytes(cols, n) : 0; }
+
+int cmolhip_act_prepare(cmolhip_ctx_t *c, const float *dx, int n, int cols, int dtype,
+                        const float *norm_w, void *op, float *ss)
+{
+    if (!c || !dx || !op || n < 1 || n > 32 || cols < 32 || cols % 32) return E_ARGS;
+    if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0) return E_UNSUPPORTED;
+    ActOut o{};
+    o.q = (_Float16 *)op;
+    o.dt = dtype;
+    o.nrows = 2 * n;
+    o.norm_w = norm_w;
+    o.ss = ss;
+    o.ss_stride = cols / 32;
+    return launch_act_prep(dx, cols, cols, n, o, c->stream);
+}
+
+int cmolhip_gemm_prepared(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op, int n,
+                          const float *ss, float eps, float *dy)
+{
+    if (!c || !w || !op || !dy || n < 1 || n > 32) return E_ARGS;
+    GemvArgs a{};
+    a.w = to_qt(*w);
+    a.in.q = (const _Float16 *)op;
+    a.in.nrows = 2 * n;
+    a.in.ss = ss;
+    a.in.ss_count = w->cols / 32;
+    a.in.ss_stride = w->cols / 32;
+    a.in.eps = eps;
+    a.out = dy;
+    a.out_stride = w->rows;
+    a.n = n;
+    return launch_gemv(a, EPI_STORE, c->stream);
+}
+
 int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx, float *dy, int n,
                  const float *norm_w, float eps)
 {
     if (!c || !w || !dx || !dy || n < 1 || n > 32) return E_ARGS;
-    for (int i = 0; i < n; i++) {
-        GemvArgs a{};
-        a.w = to_qt(*w);
-        a.x = dx + (size_t)i * w->cols;
-        a.x_stride = w->cols;
-        a.norm_w = norm_w;
-        a.eps = eps;
-        a.out = dy + (size_t)i * w->rows;
-        a.out_stride = w->rows;
-        a.n = 1;
-        RC(launch_gemv(a, EPI_STORE, c->stream));
-    }
-    return E_OK;
+    const size_t mark = arena_mark(c);
+    int rc = E_OK;
+    do {
+        void *op = nullptr;
+        float *ss = nullptr;
+        if ((rc = cmolhip_alloc(c, act_bytes(w->cols, n), ALIGN, &op))) break;
+        if (norm_w && (rc = arena_get(c, (size_t)n * (w->cols / 32), &ss))) break;
+        if ((rc = cmolhip_act_prepare(c, dx, n, w->cols, w->dtype, norm_w, op, ss))) break;
+        rc = cmolhip_gemm_prepared(c, w, op, n, ss, eps, dy);
+    } while (0);
+    arena_release(c, mark);
+    return rc;
 }
 
 int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float *b, int m, int k,
                         int n, int dtype)
 {
     if (!c || !out || !a || !b || m < 1 || k < 32 || k % 32 || n < 1 || n > 32) return E_ARGS;
-    if (!qbytes_aligned(dtype, m, k)) return E_UNSUPPORTED;
+    if (!qbytes_aligned(dtype, m, k, 1)) return E_UNSUPPORTED;
     const size_t mark = arena_mark(c);
     int rc = E_OK;
     do {
@@ -309,7 +350,7 @@ int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float
         if ((rc = arena_get(c, (size_t)m * n, &dy))) break;
         const void *parts[1] = {a};
         const int32_t rows[1] = {m};
-        if ((rc = cmolhip_qtensor_upload(c, dtype, k, 1, parts, rows, CMOLHIP_PARTS_CONCAT, staging,
+        if ((rc = cmolhip_qtensor_upload(c, dtype, k, 1, 1, parts, rows, CMOLHIP_PARTS_CONCAT, staging,
                                          rb * (size_t)m, &t)))
             break;
         std::vector<float> xt((size_t)k * n), yt((size_t)m * n);
@@ -388,16 +429,22 @@ struct MLayer {
     int rope_on = 1;
 };
 
-struct MSlot {
+// Device buffers of one decode batch of up to `cap` activation vectors.
+struct Batch {
+    int cap = 0;
     hipStream_t st = nullptr;
-    int32_t *step = nullptr;      // device {token, pos, seqlen}
-    int32_t *steps = nullptr;     // device prompt step records [max_ctx][3]
-    int32_t *slot_id = nullptr;   // device: this slot's index
-    float *x = nullptr, *q = nullptr, *ao = nullptr, *h = nullptr, *logits = nullptr;
-    unsigned long long *argmax = nullptr;
+    int32_t *steps = nullptr;       // device [cap][3] {token, pos, seqlen}
+    int32_t *slot_ids = nullptr;    // device [cap]: KV slot of each vector
+    float *x = nullptr, *q = nullptr, *logits = nullptr;
+    _Float16 *op_qkv = nullptr, *op_o = nullptr, *op_gu = nullptr, *op_dn = nullptr,
+             *op_lm = nullptr;      // consumer operands (kernels.h)
+    float *ss_a = nullptr, *ss_b = nullptr;   // sum-of-squares partials [cap][d]
+    unsigned long long *argmax = nullptr;     // [cap][ARGMAX_SLOTS]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
-    int32_t *h_steps = nullptr;   // pinned host [max_ctx][3]
-    unsigned long long *h_argmax = nullptr;
+    int32_t *prompt_steps = nullptr;          // device [max_ctx][3] (cap == 1 batches)
+    int32_t *h_steps = nullptr;               // pinned [max(cap, max_ctx)][3]
+    int32_t *h_slots = nullptr;               // pinned [cap]
+    unsigned long long *h_argmax = nullptr;   // pinned [cap][ARGMAX_SLOTS]
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     std::mutex mu;
@@ -407,7 +454,8 @@ constexpr int ATTN_SPLIT_MIN = 64, ATTN_SPLIT_MAX = 256;
 
 int pick_split(int max_ctx)
 {
-    int s = max_ctx / 64;
+    const char *e = getenv("CMOL_ATTN_SPLIT");
+    int s = e ? atoi(e) : max_ctx / 64;
     s = (s + 63) / 64 * 64;
     if (s < ATTN_SPLIT_MIN) s = ATTN_SPLIT_MIN;
     if (s > ATTN_SPLIT_MAX) s = ATTN_SPLIT_MAX;
@@ -429,14 +477,40 @@ struct Plan {
     }
 };
 
-void add_q(Plan &P, int dt, int rows, int cols)
+void add_q(Plan &P, int dt, int rows, int cols, int fold)
 {
     QLayout L;
-    qlayout(dt, rows, cols, &L);
+    qlayout(dt, rows, cols, fold, &L);
     P.add(L.qs);
     P.add(L.d);
     if (L.qh) P.add(L.qh);
 }
+
+// k parts per tile for a projection: single-session models fold matrices
+// with few rows until they make >= 512 work-groups at batch 1, as long as
+// the parts stay whole quads (padding <= 1/16); batched models keep fold 1,
+// whose tiles serve up to 8 vectors per MFMA.
+int pick_fold(int rows, int cols, int max_sessions)
+{
+    if (max_sessions > 1) return 1;
+    const int nb = cols / 32;
+    int f = 1;
+    while (f < 8 && (rows + 16 / f - 1) / (16 / f) < 512) {
+        const int nf = 2 * f;
+        if (nf * fold_quads(nb, nf) * 4 > nb + nb / 16) break;
+        f = nf;
+    }
+    return f;
+}
+
+} // namespace
+
+extern "C" int cmolhip_pick_fold(int rows, int cols, int max_sessions)
+{
+    return (rows > 0 && cols > 0 && cols % 32 == 0) ? pick_fold(rows, cols, max_sessions) : 1;
+}
+
+namespace {
 
 int validate_desc(const cmolhip_model_desc_t *d)
 {
@@ -479,13 +553,35 @@ int validate_desc(const cmolhip_model_desc_t *d)
     return E_OK;
 }
 
+// Buffers of one batch, in allocation order (mirrored by build_batch).
+void plan_batch(Plan &P, const cmolhip_hparams_t &h, int cap, int ms, int prompt)
+{
+    const size_t np = (size_t)h.n_kv_heads * ms * (h.n_heads / h.n_kv_heads);
+    P.add((size_t)cap * 3 * 4);
+    P.add((size_t)cap * 4);
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * h.vocab * 4);
+    P.add(act_bytes(h.d_model, cap));
+    P.add(act_bytes(h.d_model, cap));
+    P.add(act_bytes(h.d_model, cap));
+    P.add(act_bytes(h.d_ffn, cap));
+    P.add(act_bytes(h.d_model, cap));
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * ARGMAX_SLOTS * 8);
+    P.add((size_t)cap * np * 4);
+    P.add((size_t)cap * np * 4);
+    P.add((size_t)cap * np * h.d_head * 4);
+    if (prompt) P.add((size_t)h.max_ctx * 3 * 4);
+}
+
 Plan make_plan(const cmolhip_model_desc_t *d)
 {
     const cmolhip_hparams_t &h = d->hp;
-    const int kvd = h.n_kv_heads * h.d_head, G = h.n_heads / h.n_kv_heads;
+    const int kvd = h.n_kv_heads * h.d_head;
     const int ms = attn_max_splits(h.max_ctx, pick_split(h.max_ctx));
     Plan P;
-    // staging: largest raw tensor, capped (uploads are chunked)
     size_t big = 0;
     auto upd = [&](const cmolhip_host_tensor_t &t) {
         size_t b = raw_row_bytes(t.dtype, t.cols) * (size_t)t.rows;
@@ -501,15 +597,16 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(P.staging);
     for (int l = 0; l < h.n_layers; l++) {
         const auto &L = d->layers[l];
-        add_q(P, L.q.dtype, h.d_model + 2 * kvd, h.d_model);
-        add_q(P, L.o.dtype, h.d_model, h.d_model);
-        add_q(P, L.gate.dtype, 2 * h.d_ffn, h.d_model);
-        add_q(P, L.down.dtype, h.d_model, h.d_ffn);
+        const int ms = h.max_sessions;
+        add_q(P, L.q.dtype, h.d_model + 2 * kvd, h.d_model, pick_fold(h.d_model + 2 * kvd, h.d_model, ms));
+        add_q(P, L.o.dtype, h.d_model, h.d_model, pick_fold(h.d_model, h.d_model, ms));
+        add_q(P, L.gate.dtype, 2 * h.d_ffn, h.d_model, pick_fold(2 * h.d_ffn, h.d_model, ms));
+        add_q(P, L.down.dtype, h.d_model, h.d_ffn, pick_fold(h.d_model, h.d_ffn, ms));
         P.add((size_t)h.d_model * 4);
         P.add((size_t)h.d_model * 4);
     }
-    add_q(P, d->embd.dtype, h.vocab, h.d_model);
-    if (d->lm_head.data) add_q(P, d->lm_head.dtype, h.vocab, h.d_model);
+    add_q(P, d->embd.dtype, h.vocab, h.d_model, 1);
+    if (d->lm_head.data) add_q(P, d->lm_head.dtype, h.vocab, h.d_model, 1);
     P.add((size_t)h.d_model * 4);                                   // out_norm
     P.add((size_t)h.max_ctx * (h.d_head / 2) * 2 * 4);              // rope
     const size_t esz = h.kv_f16 ? 2 : 4;
@@ -517,21 +614,8 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(kv_elems * esz);
     P.add(kv_elems * esz);
     P.add((size_t)h.n_kv_heads * h.max_ctx * h.d_head * 4);         // scratch
-    const size_t np = (size_t)h.n_kv_heads * ms * G;
-    for (int s = 0; s < h.max_sessions; s++) {
-        P.add(16);
-        P.add((size_t)h.max_ctx * 3 * 4);
-        P.add(4);
-        P.add((size_t)h.d_model * 4);
-        P.add((size_t)h.d_model * 4);
-        P.add((size_t)h.d_model * 4);
-        P.add((size_t)h.d_ffn * 4);
-        P.add((size_t)h.vocab * 4);
-        P.add(8 * ARGMAX_SLOTS);
-        P.add(np * 4);
-        P.add(np * 4);
-        P.add(np * h.d_head * 4);
-    }
+    for (int s = 0; s < h.max_sessions; s++) plan_batch(P, h, 1, ms, 1);
+    plan_batch(P, h, h.max_sessions, ms, 0);                        // lock-step batch
     return P;
 }
 
@@ -546,40 +630,73 @@ struct cmolhip_model {
     void *kbase = nullptr, *vbase = nullptr;
     size_t slot_stride = 0, layer_stride = 0;
     int split = 64, max_splits = 1;
-    std::vector<std::unique_ptr<MSlot>> slots;
+    std::vector<std::unique_ptr<Batch>> slots;   // one single-vector batch per session
+    std::unique_ptr<Batch> multi;                // lock-step batch over sessions
     std::mutex scratch_mu;
     bool use_graph = true;
 };
 
 namespace {
 
-KVRef kvref(const cmolhip_model *m, const MSlot &S, int layer)
+KVRef kvref(const cmolhip_model *m, const Batch &B, int layer)
 {
     KVRef r;
     r.k_base = m->kbase;
     r.v_base = m->vbase;
     r.slot_stride = m->slot_stride;
     r.layer_off = (size_t)layer * m->layer_stride;
-    r.slot_ids = S.slot_id;
+    r.slot_ids = B.slot_ids;
     return r;
 }
 
-int enqueue_decode(cmolhip_model *m, MSlot &S, hipStream_t st)
+ActOut act_out(_Float16 *q, int dt, int n, const float *norm_w, float *ss, int ss_stride)
+{
+    ActOut o{};
+    o.q = q;
+    o.dt = dt;
+    o.nrows = 2 * n;
+    o.norm_w = norm_w;
+    o.ss = norm_w ? ss : nullptr;
+    o.ss_stride = ss_stride;
+    return o;
+}
+
+ActIn act_in(const _Float16 *q, int n, const float *ss, int count, int stride, float eps)
+{
+    ActIn i{};
+    i.q = q;
+    i.nrows = 2 * n;
+    i.ss = ss;
+    i.ss_count = count;
+    i.ss_stride = stride;
+    i.eps = eps;
+    return i;
+}
+
+const cmolhip_qtensor_t &lm_tensor(const cmolhip_model *m) { return m->lm.qs ? m->lm : m->embd; }
+
+// One decode step of n vectors of batch B (reference cmol_model_forward per
+// vector): embedding, L x (QKV+RoPE+KV write, attention, Wo + residual,
+// gate/up + SwiGLU, down + residual), LM head + argmax.
+int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
 {
     const cmolhip_hparams_t &hp = m->hp;
-    const int d = hp.d_model, kvd = hp.n_kv_heads * hp.d_head;
-    RC(launch_embed(to_qt(m->embd), S.step, 3, S.x, d, S.argmax, 1, st));
+    // sum-of-squares partials: one per 32 inputs from the embedding, one per
+    // row tile from a residual epilogue; stride d covers both
+    const int d = hp.d_model, kvd = hp.n_kv_heads * hp.d_head, P = d;
+    const float eps = hp.rms_eps;
+    RC(launch_embed(to_qt(m->embd), B.steps, 3, B.x, d,
+                    act_out(B.op_qkv, m->layers[0].qkv.dtype, n, m->layers[0].attn_norm, B.ss_a, P),
+                    B.argmax, n, st));
+    int ss_count = d / 32;   // the embedding writes one partial per 32 inputs
     for (int l = 0; l < hp.n_layers; l++) {
         const MLayer &L = m->layers[l];
         GemvArgs g{};
         g.w = to_qt(L.qkv);
-        g.x = S.x;
-        g.x_stride = d;
-        g.norm_w = L.attn_norm;
-        g.eps = hp.rms_eps;
-        g.out = S.q;
+        g.in = act_in(B.op_qkv, n, B.ss_a, ss_count, P, eps);
+        g.out = B.q;
         g.out_stride = d;
-        g.n = 1;
+        g.n = n;
         g.nq = d;
         g.nkv = kvd;
         g.d_head = hp.d_head;
@@ -587,18 +704,18 @@ int enqueue_decode(cmolhip_model *m, MSlot &S, hipStream_t st)
         g.kv_f16 = hp.kv_f16;
         g.rope_on = L.rope_on;
         g.rope = m->rope;
-        g.kv = kvref(m, S, l);
-        g.pos = S.step + 1;
+        g.kv = kvref(m, B, l);
+        g.pos = B.steps + 1;
         g.pos_stride = 3;
         RC(launch_gemv(g, EPI_QKV, st));
 
         AttnArgs at{};
-        at.q = S.q;
+        at.q = B.q;
         at.q_stride = d;
-        at.kv = kvref(m, S, l);
-        at.seqlen = S.step + 2;
+        at.kv = kvref(m, B, l);
+        at.seqlen = B.steps + 2;
         at.seqlen_stride = 3;
-        at.n = 1;
+        at.n = n;
         at.n_heads = hp.n_heads;
         at.n_kv = hp.n_kv_heads;
         at.d_head = hp.d_head;
@@ -606,52 +723,50 @@ int enqueue_decode(cmolhip_model *m, MSlot &S, hipStream_t st)
         at.kv_f16 = hp.kv_f16;
         at.split = m->split;
         at.max_splits = m->max_splits;
-        at.pm = S.pm;
-        at.pl = S.pl;
-        at.po = S.po;
-        at.out = S.ao;
-        at.out_stride = d;
+        at.pm = B.pm;
+        at.pl = B.pl;
+        at.po = B.po;
+        at.out = nullptr;
+        at.next = act_out(B.op_o, L.o.dtype, n, nullptr, nullptr, 0);
         RC(launch_attn(at, st));
 
         GemvArgs go{};
         go.w = to_qt(L.o);
-        go.x = S.ao;
-        go.x_stride = d;
-        go.out = S.x;
+        go.in = act_in(B.op_o, n, nullptr, 0, 0, eps);
+        go.out = B.x;
         go.out_stride = d;
-        go.n = 1;
+        go.n = n;
+        go.next = act_out(B.op_gu, L.gu.dtype, n, L.ffn_norm, B.ss_b, P);
         RC(launch_gemv(go, EPI_RESID, st));
 
         GemvArgs gu{};
         gu.w = to_qt(L.gu);
-        gu.x = S.x;
-        gu.x_stride = d;
-        gu.norm_w = L.ffn_norm;
-        gu.eps = hp.rms_eps;
-        gu.out = S.h;
-        gu.out_stride = hp.d_ffn;
-        gu.n = 1;
+        gu.in = act_in(B.op_gu, n, B.ss_b, L.o.row_tiles, P, eps);
+        gu.out = nullptr;
+        gu.n = n;
+        gu.next = act_out(B.op_dn, L.down.dtype, n, nullptr, nullptr, 0);
         RC(launch_gemv(gu, EPI_SWIGLU, st));
 
         GemvArgs gd{};
         gd.w = to_qt(L.down);
-        gd.x = S.h;
-        gd.x_stride = hp.d_ffn;
-        gd.out = S.x;
+        gd.in = act_in(B.op_dn, n, nullptr, 0, 0, eps);
+        gd.out = B.x;
         gd.out_stride = d;
-        gd.n = 1;
+        gd.n = n;
+        if (l + 1 < hp.n_layers)
+            gd.next = act_out(B.op_qkv, m->layers[l + 1].qkv.dtype, n, m->layers[l + 1].attn_norm, B.ss_a, P);
+        else
+            gd.next = act_out(B.op_lm, lm_tensor(m).dtype, n, m->out_norm, B.ss_a, P);
         RC(launch_gemv(gd, EPI_RESID, st));
+        ss_count = L.down.row_tiles;
     }
     GemvArgs gl{};
-    gl.w = to_qt(m->lm.qs ? m->lm : m->embd);
-    gl.x = S.x;
-    gl.x_stride = d;
-    gl.norm_w = m->out_norm;
-    gl.eps = hp.rms_eps;
-    gl.out = S.logits;
+    gl.w = to_qt(lm_tensor(m));
+    gl.in = act_in(B.op_lm, n, B.ss_a, ss_count, P, eps);
+    gl.out = B.logits;
     gl.out_stride = hp.vocab;
-    gl.n = 1;
-    gl.argmax = S.argmax;
+    gl.n = n;
+    gl.argmax = B.argmax;
     RC(launch_gemv(gl, EPI_LOGITS, st));
     return E_OK;
 }
@@ -662,8 +777,8 @@ int upload_norm(cmolhip_ctx_t *c, const cmolhip_host_tensor_t &t, float **dst)
     return cmolhip_memcpy_h2d(c, *dst, t.data, (size_t)t.cols * 4);
 }
 
-int upload_q(cmolhip_ctx_t *c, int n, const cmolhip_host_tensor_t *const *ts, int mode, void *stg,
-             size_t stg_bytes, cmolhip_qtensor_t *out)
+int upload_q(cmolhip_ctx_t *c, int n, const cmolhip_host_tensor_t *const *ts, int mode, int fold,
+             void *stg, size_t stg_bytes, cmolhip_qtensor_t *out)
 {
     const void *parts[3];
     int32_t rows[3];
@@ -671,38 +786,74 @@ int upload_q(cmolhip_ctx_t *c, int n, const cmolhip_host_tensor_t *const *ts, in
         parts[i] = ts[i]->data;
         rows[i] = ts[i]->rows;
     }
-    return cmolhip_qtensor_upload(c, ts[0]->dtype, ts[0]->cols, n, parts, rows, mode, stg, stg_bytes, out);
+    return cmolhip_qtensor_upload(c, ts[0]->dtype, ts[0]->cols, fold, n, parts, rows, mode, stg, stg_bytes, out);
+}
+
+int build_batch(cmolhip_model *m, Batch &B, int cap, int prompt)
+{
+    cmolhip_ctx_t *c = m->ctx;
+    const cmolhip_hparams_t &h = m->hp;
+    const size_t np = (size_t)h.n_kv_heads * m->max_splits * (h.n_heads / h.n_kv_heads);
+    B.cap = cap;
+    RC(arena_get(c, (size_t)cap * 3, &B.steps));
+    RC(arena_get(c, (size_t)cap, &B.slot_ids));
+    RC(arena_get(c, (size_t)cap * h.d_model, &B.x));
+    RC(arena_get(c, (size_t)cap * h.d_model, &B.q));
+    RC(arena_get(c, (size_t)cap * h.vocab, &B.logits));
+    _Float16 **ops[5] = {&B.op_qkv, &B.op_o, &B.op_gu, &B.op_dn, &B.op_lm};
+    const int opk[5] = {h.d_model, h.d_model, h.d_model, h.d_ffn, h.d_model};
+    for (int i = 0; i < 5; i++) {
+        const size_t nb = act_bytes(opk[i], cap);
+        RC(cmolhip_alloc(c, nb, ALIGN, (void **)ops[i]));
+    }
+    RC(arena_get(c, (size_t)cap * h.d_model, &B.ss_a));
+    RC(arena_get(c, (size_t)cap * h.d_model, &B.ss_b));
+    RC(arena_get(c, (size_t)cap * ARGMAX_SLOTS, &B.argmax));
+    RC(arena_get(c, (size_t)cap * np, &B.pm));
+    RC(arena_get(c, (size_t)cap * np, &B.pl));
+    RC(arena_get(c, (size_t)cap * np * h.d_head, &B.po));
+    if (prompt) RC(arena_get(c, (size_t)h.max_ctx * 3, &B.prompt_steps));
+    HC(hipMemsetAsync(B.steps, 0, (size_t)cap * 12, c->stream));
+    HC(hipStreamCreateWithFlags(&B.st, hipStreamNonBlocking));
+    const size_t hs = (size_t)(prompt ? (h.max_ctx > cap ? h.max_ctx : cap) : cap) * 3 * 4;
+    HC(hipHostMalloc((void **)&B.h_steps, hs, hipHostMallocDefault));
+    HC(hipHostMalloc((void **)&B.h_slots, (size_t)cap * 4, hipHostMallocDefault));
+    HC(hipHostMalloc((void **)&B.h_argmax, (size_t)cap * ARGMAX_SLOTS * 8, hipHostMallocDefault));
+    return E_OK;
 }
 
 int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
 {
     cmolhip_ctx_t *c = m->ctx;
     const cmolhip_hparams_t &h = d->hp;
-    const int kvd = h.n_kv_heads * h.d_head, G = h.n_heads / h.n_kv_heads;
     void *stg = nullptr;
     RC(cmolhip_alloc(c, P.staging, ALIGN, &stg));
     m->layers.resize(h.n_layers);
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &T = d->layers[l];
         MLayer &L = m->layers[l];
+        const int ms = h.max_sessions, kvd = h.n_kv_heads * h.d_head;
         const cmolhip_host_tensor_t *qkv[3] = {&T.q, &T.k, &T.v};
-        RC(upload_q(c, 3, qkv, CMOLHIP_PARTS_CONCAT, stg, P.staging, &L.qkv));
+        RC(upload_q(c, 3, qkv, CMOLHIP_PARTS_CONCAT, pick_fold(h.d_model + 2 * kvd, h.d_model, ms),
+                    stg, P.staging, &L.qkv));
         const cmolhip_host_tensor_t *o[1] = {&T.o};
-        RC(upload_q(c, 1, o, CMOLHIP_PARTS_CONCAT, stg, P.staging, &L.o));
+        RC(upload_q(c, 1, o, CMOLHIP_PARTS_CONCAT, pick_fold(h.d_model, h.d_model, ms), stg,
+                    P.staging, &L.o));
         const cmolhip_host_tensor_t *gu[2] = {&T.gate, &T.up};
-        RC(upload_q(c, 2, gu, CMOLHIP_PARTS_INTERLEAVE, stg, P.staging, &L.gu));
+        RC(upload_q(c, 2, gu, CMOLHIP_PARTS_INTERLEAVE, pick_fold(2 * h.d_ffn, h.d_model, ms), stg,
+                    P.staging, &L.gu));
         const cmolhip_host_tensor_t *dn[1] = {&T.down};
-        RC(upload_q(c, 1, dn, CMOLHIP_PARTS_CONCAT, stg, P.staging, &L.down));
+        RC(upload_q(c, 1, dn, CMOLHIP_PARTS_CONCAT, pick_fold(h.d_model, h.d_ffn, ms), stg,
+                    P.staging, &L.down));
         RC(upload_norm(c, T.attn_norm, &L.attn_norm));
         RC(upload_norm(c, T.ffn_norm, &L.ffn_norm));
         L.rope_on = !(h.no_rope_interval > 0 && (l + 1) % h.no_rope_interval == 0);
     }
-    (void)kvd;
     const cmolhip_host_tensor_t *e[1] = {&d->embd};
-    RC(upload_q(c, 1, e, CMOLHIP_PARTS_CONCAT, stg, P.staging, &m->embd));
+    RC(upload_q(c, 1, e, CMOLHIP_PARTS_CONCAT, 1, stg, P.staging, &m->embd));
     if (d->lm_head.data) {
         const cmolhip_host_tensor_t *lh[1] = {&d->lm_head};
-        RC(upload_q(c, 1, lh, CMOLHIP_PARTS_CONCAT, stg, P.staging, &m->lm));
+        RC(upload_q(c, 1, lh, CMOLHIP_PARTS_CONCAT, 1, stg, P.staging, &m->lm));
     }
     RC(upload_norm(c, d->out_norm, &m->out_norm));
     const size_t rope_n = (size_t)h.max_ctx * (h.d_head / 2) * 2;
@@ -719,39 +870,25 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     RC(arena_get(c, (size_t)h.n_kv_heads * h.max_ctx * h.d_head, &m->scratch));
     m->split = pick_split(h.max_ctx);
     m->max_splits = attn_max_splits(h.max_ctx, m->split);
-    const size_t np = (size_t)h.n_kv_heads * m->max_splits * G;
     for (int s = 0; s < h.max_sessions; s++) {
-        m->slots.emplace_back(new MSlot());
-        MSlot &S = *m->slots.back();
-        RC(arena_get(c, 4, &S.step));
-        RC(arena_get(c, (size_t)h.max_ctx * 3, &S.steps));
-        RC(arena_get(c, 1, &S.slot_id));
-        RC(arena_get(c, (size_t)h.d_model, &S.x));
-        RC(arena_get(c, (size_t)h.d_model, &S.q));
-        RC(arena_get(c, (size_t)h.d_model, &S.ao));
-        RC(arena_get(c, (size_t)h.d_ffn, &S.h));
-        RC(arena_get(c, (size_t)h.vocab, &S.logits));
-        RC(arena_get(c, ARGMAX_SLOTS, &S.argmax));
-        RC(arena_get(c, np, &S.pm));
-        RC(arena_get(c, np, &S.pl));
-        RC(arena_get(c, np * h.d_head, &S.po));
-        HC(hipMemsetAsync(S.step, 0, 16, c->stream));
-        int32_t sid = s;
-        RC(cmolhip_memcpy_h2d(c, S.slot_id, &sid, 4));
-        HC(hipStreamCreateWithFlags(&S.st, hipStreamNonBlocking));
-        HC(hipHostMalloc((void **)&S.h_steps, (size_t)h.max_ctx * 3 * 4, hipHostMallocDefault));
-        HC(hipHostMalloc((void **)&S.h_argmax, 8 * ARGMAX_SLOTS, hipHostMallocDefault));
+        m->slots.emplace_back(new Batch());
+        Batch &B = *m->slots.back();
+        RC(build_batch(m, B, 1, 1));
+        const int32_t sid = s;
+        RC(cmolhip_memcpy_h2d(c, B.slot_ids, &sid, 4));
     }
+    m->multi.reset(new Batch());
+    RC(build_batch(m, *m->multi, h.max_sessions, 0));
     HC(hipStreamSynchronize(c->stream));
     if (m->use_graph) {
         for (auto &sp : m->slots) {
-            MSlot &S = *sp;
-            HC(hipStreamBeginCapture(S.st, hipStreamCaptureModeThreadLocal));
-            int rc = enqueue_decode(m, S, S.st);
-            hipError_t ce = hipStreamEndCapture(S.st, &S.graph);
+            Batch &B = *sp;
+            HC(hipStreamBeginCapture(B.st, hipStreamCaptureModeThreadLocal));
+            int rc = enqueue_step(m, B, 1, B.st);
+            hipError_t ce = hipStreamEndCapture(B.st, &B.graph);
             if (rc) return rc;
             HC(ce);
-            HC(hipGraphInstantiate(&S.gexec, S.graph, nullptr, nullptr, 0));
+            HC(hipGraphInstantiate(&B.gexec, B.graph, nullptr, nullptr, 0));
         }
     }
     return E_OK;
@@ -764,23 +901,36 @@ unsigned long long reduce_slots(const unsigned long long *k)
     return best;
 }
 
-int run_step(cmolhip_model *m, MSlot &S)
+int run_single(cmolhip_model *m, Batch &B)
 {
-    if (S.gexec) {
-        HC(hipGraphLaunch(S.gexec, S.st));
+    if (B.gexec) {
+        HC(hipGraphLaunch(B.gexec, B.st));
         return E_OK;
     }
-    return enqueue_decode(m, S, S.st);
+    return enqueue_step(m, B, 1, B.st);
 }
 
-int finish_step(cmolhip_model *m, MSlot &S, float *logits_host, int32_t *argmax)
+int finish(cmolhip_model *m, Batch &B, int n, float *logits_host, int32_t *argmax)
 {
-    HC(hipMemcpyAsync(S.h_argmax, S.argmax, 8 * ARGMAX_SLOTS, hipMemcpyDeviceToHost, S.st));
+    HC(hipMemcpyAsync(B.h_argmax, B.argmax, (size_t)n * ARGMAX_SLOTS * 8, hipMemcpyDeviceToHost, B.st));
     if (logits_host)
-        HC(hipMemcpyAsync(logits_host, S.logits, (size_t)m->hp.vocab * 4, hipMemcpyDeviceToHost, S.st));
-    HC(hipStreamSynchronize(S.st));
-    if (argmax) *argmax = (int32_t)argmax_index(reduce_slots(S.h_argmax));
+        HC(hipMemcpyAsync(logits_host, B.logits, (size_t)n * m->hp.vocab * 4, hipMemcpyDeviceToHost, B.st));
+    HC(hipStreamSynchronize(B.st));
+    if (argmax)
+        for (int i = 0; i < n; i++)
+            argmax[i] = (int32_t)argmax_index(reduce_slots(B.h_argmax + (size_t)i * ARGMAX_SLOTS));
     return E_OK;
+}
+
+void destroy_batch(Batch &B)
+{
+    if (B.st) (void)hipStreamSynchronize(B.st);
+    if (B.gexec) (void)hipGraphExecDestroy(B.gexec);
+    if (B.graph) (void)hipGraphDestroy(B.graph);
+    if (B.st) (void)hipStreamDestroy(B.st);
+    if (B.h_steps) (void)hipHostFree(B.h_steps);
+    if (B.h_slots) (void)hipHostFree(B.h_slots);
+    if (B.h_argmax) (void)hipHostFree(B.h_argmax);
 }
 
 } // namespace
@@ -819,16 +969,9 @@ int cmolhip_model_create(const cmolhip_model_desc_t *desc, int device, cmolhip_m
 void cmolhip_model_destroy(cmolhip_model_t *m)
 {
     if (!m) return;
-    if (m->ctx) hipSetDevice(m->ctx->device);
-    for (auto &sp : m->slots) {
-        MSlot &S = *sp;
-        if (S.st) hipStreamSynchronize(S.st);
-        if (S.gexec) hipGraphExecDestroy(S.gexec);
-        if (S.graph) hipGraphDestroy(S.graph);
-        if (S.st) hipStreamDestroy(S.st);
-        if (S.h_steps) hipHostFree(S.h_steps);
-        if (S.h_argmax) hipHostFree(S.h_argmax);
-    }
+    if (m->ctx) (void)hipSetDevice(m->ctx->device);
+    for (auto &sp : m->slots) destroy_batch(*sp);
+    if (m->multi) destroy_batch(*m->multi);
     cmolhip_ctx_destroy(m->ctx);
     delete m;
 }
@@ -846,14 +989,14 @@ int cmolhip_decode(cmolhip_model_t *m, int slot, int32_t token, int32_t pos, flo
 {
     if (!m || slot < 0 || slot >= (int)m->slots.size()) return E_ARGS;
     if (token < 0 || token >= m->hp.vocab || pos < 0 || pos >= m->hp.max_ctx) return E_ARGS;
-    MSlot &S = *m->slots[slot];
-    std::lock_guard<std::mutex> g(S.mu);
-    S.h_steps[0] = token;
-    S.h_steps[1] = pos;
-    S.h_steps[2] = pos + 1;
-    HC(hipMemcpyAsync(S.step, S.h_steps, 12, hipMemcpyHostToDevice, S.st));
-    RC(run_step(m, S));
-    return finish_step(m, S, logits_host, argmax);
+    Batch &B = *m->slots[slot];
+    std::lock_guard<std::mutex> g(B.mu);
+    B.h_steps[0] = token;
+    B.h_steps[1] = pos;
+    B.h_steps[2] = pos + 1;
+    HC(hipMemcpyAsync(B.steps, B.h_steps, 12, hipMemcpyHostToDevice, B.st));
+    RC(run_single(m, B));
+    return finish(m, B, 1, logits_host, argmax);
 }
 
 int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, int32_t pos0,
@@ -863,25 +1006,25 @@ int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, 
     if (pos0 < 0 || (long)pos0 + n > m->hp.max_ctx) return E_ARGS;
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->hp.vocab) return E_ARGS;
-    MSlot &S = *m->slots[slot];
-    std::lock_guard<std::mutex> g(S.mu);
+    Batch &B = *m->slots[slot];
+    std::lock_guard<std::mutex> g(B.mu);
     for (int i = 0; i < n; i++) {
-        S.h_steps[3 * i + 0] = tokens[i];
-        S.h_steps[3 * i + 1] = pos0 + i;
-        S.h_steps[3 * i + 2] = pos0 + i + 1;
+        B.h_steps[3 * i + 0] = tokens[i];
+        B.h_steps[3 * i + 1] = pos0 + i;
+        B.h_steps[3 * i + 2] = pos0 + i + 1;
     }
-    HC(hipMemcpyAsync(S.steps, S.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, S.st));
+    HC(hipMemcpyAsync(B.prompt_steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
     for (int i = 0; i < n; i++) {
-        HC(hipMemcpyAsync(S.step, S.steps + 3 * i, 12, hipMemcpyDeviceToDevice, S.st));
-        RC(run_step(m, S));
+        HC(hipMemcpyAsync(B.steps, B.prompt_steps + 3 * i, 12, hipMemcpyDeviceToDevice, B.st));
+        RC(run_single(m, B));
     }
-    return finish_step(m, S, logits_host, argmax);
+    return finish(m, B, 1, logits_host, argmax);
 }
 
 int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t *tokens,
                          const int32_t *pos, float *logits_host, int32_t *argmax)
 {
-    if (!m || n < 1 || !slots || !tokens || !pos) return E_ARGS;
+    if (!m || n < 1 || n > m->hp.max_sessions || !slots || !tokens || !pos) return E_ARGS;
     for (int i = 0; i < n; i++) {
         if (slots[i] < 0 || slots[i] >= (int)m->slots.size()) return E_ARGS;
         if (tokens[i] < 0 || tokens[i] >= m->hp.vocab || pos[i] < 0 || pos[i] >= m->hp.max_ctx)
@@ -889,37 +1032,23 @@ int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const 
         for (int j = 0; j < i; j++)
             if (slots[j] == slots[i]) return E_ARGS;
     }
+    Batch &B = *m->multi;
+    std::lock_guard<std::mutex> g(B.mu);
+    // the KV caches of these sessions are written: exclude their own decodes
+    std::vector<std::unique_lock<std::mutex>> held;
+    std::vector<int> order(slots, slots + n);
+    std::sort(order.begin(), order.end());
+    for (int s : order) held.emplace_back(m->slots[s]->mu);
     for (int i = 0; i < n; i++) {
-        MSlot &S = *m->slots[slots[i]];
-        S.mu.lock();
-        S.h_steps[0] = tokens[i];
-        S.h_steps[1] = pos[i];
-        S.h_steps[2] = pos[i] + 1;
-        hipError_t e = hipMemcpyAsync(S.step, S.h_steps, 12, hipMemcpyHostToDevice, S.st);
-        int rc = e == hipSuccess ? run_step(m, S) : herr(e);
-        if (rc == E_OK) {
-            e = hipMemcpyAsync(S.h_argmax, S.argmax, 8 * ARGMAX_SLOTS, hipMemcpyDeviceToHost, S.st);
-            if (e == hipSuccess && logits_host)
-                e = hipMemcpyAsync(logits_host + (size_t)i * m->hp.vocab, S.logits,
-                                   (size_t)m->hp.vocab * 4, hipMemcpyDeviceToHost, S.st);
-            rc = herr(e);
-        }
-        if (rc != E_OK) {
-            for (int j = 0; j <= i; j++) {
-                hipStreamSynchronize(m->slots[slots[j]]->st);
-                m->slots[slots[j]]->mu.unlock();
-            }
-            return rc;
-        }
+        B.h_steps[3 * i + 0] = tokens[i];
+        B.h_steps[3 * i + 1] = pos[i];
+        B.h_steps[3 * i + 2] = pos[i] + 1;
+        B.h_slots[i] = slots[i];
     }
-    int rc = E_OK;
-    for (int i = 0; i < n; i++) {
-        MSlot &S = *m->slots[slots[i]];
-        if (hipStreamSynchronize(S.st) != hipSuccess) rc = E_INVALID;
-        if (argmax) argmax[i] = (int32_t)argmax_index(reduce_slots(S.h_argmax));
-        S.mu.unlock();
-    }
-    return rc;
+    HC(hipMemcpyAsync(B.steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
+    HC(hipMemcpyAsync(B.slot_ids, B.h_slots, (size_t)n * 4, hipMemcpyHostToDevice, B.st));
+    RC(enqueue_step(m, B, n, B.st));
+    return finish(m, B, n, logits_host, argmax);
 }
 
 int cmolhip_kv_download(cmolhip_model_t *m, int slot, int layer, int n, float *k_out, float *v_out)
@@ -933,7 +1062,8 @@ int cmolhip_kv_download(cmolhip_model_t *m, int slot, int layer, int n, float *k
     const size_t cnt = (size_t)n * h.n_kv_heads * h.d_head;
     std::lock_guard<std::mutex> g(m->scratch_mu);
     hipStream_t st = m->ctx->stream;
-    hipStreamSynchronize(m->slots[slot]->st);
+    HC(hipStreamSynchronize(m->slots[slot]->st));
+    HC(hipStreamSynchronize(m->multi->st));
     for (int w = 0; w < 2; w++) {
         const uint8_t *src = (const uint8_t *)(w ? m->vbase : m->kbase) + off;
         RC(launch_kv_convert(src, m->scratch, h.n_kv_heads, h.max_ctx, h.d_head, n, h.kv_f16, 1, st));
@@ -954,7 +1084,8 @@ int cmolhip_kv_upload(cmolhip_model_t *m, int slot, int layer, int n, const floa
     const size_t cnt = (size_t)n * h.n_kv_heads * h.d_head;
     std::lock_guard<std::mutex> g(m->scratch_mu);
     hipStream_t st = m->ctx->stream;
-    hipStreamSynchronize(m->slots[slot]->st);
+    HC(hipStreamSynchronize(m->slots[slot]->st));
+    HC(hipStreamSynchronize(m->multi->st));
     for (int w = 0; w < 2; w++) {
         uint8_t *dst = (uint8_t *)(w ? m->vbase : m->kbase) + off;
         RC(cmolhip_memcpy_h2d(m->ctx, m->scratch, w ? v_in : k_in, cnt * 4));
@@ -970,7 +1101,8 @@ int cmolhip_kv_fill_synthetic(cmolhip_model_t *m, int slot, int n, uint64_t seed
     const cmolhip_hparams_t &h = m->hp;
     const size_t esz = h.kv_f16 ? 2 : 4;
     hipStream_t st = m->ctx->stream;
-    hipStreamSynchronize(m->slots[slot]->st);
+    HC(hipStreamSynchronize(m->slots[slot]->st));
+    HC(hipStreamSynchronize(m->multi->st));
     for (int l = 0; l < h.n_layers; l++) {
         const size_t off = ((size_t)slot * m->slot_stride + (size_t)l * m->layer_stride) * esz;
         RC(launch_kv_synth((uint8_t *)m->kbase + off, (uint8_t *)m->vbase + off, h.n_kv_heads,

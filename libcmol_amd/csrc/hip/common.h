@@ -17,26 +17,35 @@ enum { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q5_0 = 6, DT_Q8_0 = 8 };
 // ---------------------------------------------------------------------------
 // Tiled weight layout ("quad tiles").
 //
-// A GGUF block tensor of M rows x K cols (nb = K/32 blocks per row) is stored
-// as RT = ceil(M/16) row tiles x BQ = ceil(nb/4) block quads.  Within a
-// (tile t, quad q) cell every one of the 64 lanes of a wavefront owns the
-// codes it feeds to one v_mfma_f32_16x16x32_f16 as its B operand:
-//   lane l  ->  weight row 16t + (l % 16), k-group g = l / 16
-//   Q4_0/Q5_0: 16 bytes = dword g of the 16-byte nibble array of blocks
-//              4q..4q+3 (4 bytes per block)
-//   Q8_0:      32 bytes = bytes 8g..8g+7 of the 32 int8 codes of blocks
-//              4q..4q+3 (8 bytes per block)
+// A GGUF block tensor of M rows x K cols (nb = K/32 blocks per row) with fold
+// F in {1, 2, 4, 8} is cut into RT = ceil(M/R) row tiles of R = 16/F rows
+// and, along k, into F parts of BQ quads (4 blocks) each, BQ = ceil(ceil(nb/F)
+// / 4); part p covers blocks [4*BQ*p, 4*BQ*(p+1)).  A (tile t, quad q) cell
+// has 16 columns, the 16 B-operand columns of v_mfma_f32_16x16x32_f16:
+//   column c -> weight row R*t + c % R, part c / R, blocks 4*BQ*(c/R)+4q+bi
+// and every one of the 64 lanes of a wavefront owns the codes it feeds to
+// the MFMA:  lane l -> column l % 16, k-group g = l / 16,
+//   Q4_0/Q5_0: 16 bytes = dword g of the 16-byte nibble array of each of the
+//              cell's 4 blocks (4 bytes per block)
+//   Q8_0:      32 bytes = bytes 8g..8g+7 of the 32 int8 codes of each of the
+//              4 blocks (8 bytes per block)
 // so one wave-wide 16-byte (or 2x16-byte) load per lane moves a contiguous
-// 1 KiB (2 KiB).  Scales: 16 rows x 4 blocks fp16 per cell (128 bytes),
-// entry [row % 16][block % 4].  Q5_0 fifth bits: one dword per lane per cell,
+// 1 KiB (2 KiB).  Scales: 16 columns x 4 blocks fp16 per cell (128 bytes),
+// entry [column][block % 4].  Q5_0 fifth bits: one dword per lane per cell,
 // byte (block % 4) holding the 8 fifth bits of the lane's 8 codes in pair
 // order (see deq_q5).  Rows beyond M and blocks beyond nb are zero-filled.
+// F = 1 is the plain layout (16 rows per tile); F > 1 lets a matrix with
+// few rows spread over F times more work-groups at batch 1.
 //
 // k order inside a block for lane group g, element e (the same permutation is
 // applied to the activation operand, so the MFMA contraction is unchanged):
 //   Q4_0/Q5_0: e -> (e>=4 ? 16 : 0) + 4g + {0,2,1,3}[e&3]
 //   Q8_0:      e -> 8g + e
 // ---------------------------------------------------------------------------
+
+__host__ __device__ inline bool fold_ok(int f) { return f == 1 || f == 2 || f == 4 || f == 8; }
+// block quads per k part
+__host__ __device__ inline int fold_quads(int nb, int f) { return ((nb + f - 1) / f + 3) / 4; }
 
 template <int DT> struct QFmt;
 template <> struct QFmt<DT_Q4_0> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 18; };
@@ -70,15 +79,31 @@ __device__ inline f16x8 pack8(f16x2 a, f16x2 b, f16x2 c, f16x2 d)
 // for n < 1024, so OR-ing a nibble/byte under that exponent and subtracting
 // the bias in packed f16 yields the signed code exactly.
 
-// Q4_0: dword D holds bytes b0..b3; value = nibble - 8.
+// Q4_0: dword D holds 8 nibbles; the low/high nibble of each 16-bit half is
+// placed under the exponent of 1024 (0x6400): 1024 + n, or 1024 + 16 n for
+// the upper nibble (rescaled by the packed fma), then the bias 1024 + 8 is
+// removed.  Element order [n@0, n@16, n@8, n@24, n@4, n@20, n@12, n@28]
+// (bit positions in D), which is the kmap order.  All steps are exact.
+__device__ inline uint32_t magic_1024()
+{
+    uint32_t m = 0x64006400u;
+    asm volatile("" : "+v"(m));   // keep in a VGPR so and-or fuses
+    return m;
+}
+
 __device__ inline f16x8 deq_q4(uint32_t D)
 {
+    const uint32_t m = magic_1024();
     const f16x2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    uint32_t p0 = (D & 0x000F000Fu) | 0x64006400u;
-    uint32_t p1 = ((D >> 8) & 0x000F000Fu) | 0x64006400u;
-    uint32_t p2 = ((D >> 4) & 0x000F000Fu) | 0x64006400u;
-    uint32_t p3 = ((D >> 12) & 0x000F000Fu) | 0x64006400u;
-    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) + bias, as_h2(p3) + bias);
+    const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const f16x2 bias16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const uint32_t Dh = D >> 8;
+    const uint32_t p0 = (D & 0x000F000Fu) | m;
+    const uint32_t p1 = (Dh & 0x000F000Fu) | m;
+    const uint32_t p2 = (D & 0x00F000F0u) | m;
+    const uint32_t p3 = (Dh & 0x00F000F0u) | m;
+    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) * s16 + bias16,
+                 as_h2(p3) * s16 + bias16);
 }
 
 // Q5_0: nibbles as Q4_0 plus fifth bits; hb = the lane's byte for this block
@@ -86,13 +111,18 @@ __device__ inline f16x8 deq_q4(uint32_t D)
 // value = (nibble | fifth << 4) - 16.
 __device__ inline f16x8 deq_q5(uint32_t D, uint32_t hb)
 {
+    const uint32_t m = magic_1024();
     const f16x2 bias = {(_Float16)-1040.0f, (_Float16)-1040.0f};
-    uint32_t hs = ((hb & 0x0Fu) << 4) | ((hb & 0xF0u) << 16);
-    uint32_t p0 = (D & 0x000F000Fu) | 0x64006400u | (hs & 0x00100010u);
-    uint32_t p1 = ((D >> 8) & 0x000F000Fu) | 0x64006400u | ((hs >> 1) & 0x00100010u);
-    uint32_t p2 = ((D >> 4) & 0x000F000Fu) | 0x64006400u | ((hs >> 2) & 0x00100010u);
-    uint32_t p3 = ((D >> 12) & 0x000F000Fu) | 0x64006400u | ((hs >> 3) & 0x00100010u);
-    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) + bias, as_h2(p3) + bias);
+    const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const f16x2 bias16 = {(_Float16)-80.0f, (_Float16)-80.0f};
+    const uint32_t hs = ((hb & 0x0Fu) << 4) | ((hb & 0xF0u) << 16);
+    const uint32_t Dh = D >> 8;
+    const uint32_t p0 = (D & 0x000F000Fu) | m | (hs & 0x00100010u);
+    const uint32_t p1 = (Dh & 0x000F000Fu) | m | ((hs >> 1) & 0x00100010u);
+    const uint32_t p2 = (D & 0x00F000F0u) | m | ((hs << 2) & 0x01000100u);
+    const uint32_t p3 = (Dh & 0x00F000F0u) | m | ((hs << 1) & 0x01000100u);
+    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) * s16 + bias16,
+                 as_h2(p3) * s16 + bias16);
 }
 
 // Q8_0: two dwords of int8 codes; flip the sign bit (b+128 in 0..255),

@@ -1,0 +1,464 @@
+// gemv_impl.h — the quantised matvec kernel template (see gemv.hip) and its
+// per-format launchers; instantiated once per weight format by
+// gemv_q4.hip / gemv_q5.hip / gemv_q8.hip so the three compile in parallel.
+#pragma once
+#include "common.h"
+#include "kernels.h"
+
+#include <cstdlib>
+
+// Launch shape of one matvec (host-computed, see plan_gemv).
+struct GemvShape {
+    int epi;        // GemvEpilogue
+    int qpc;        // quads per wave per operand chunk
+    int op_bytes;   // LDS bytes of the operand area (staged blocks + zero slot)
+    int zslot;      // LDS byte offset of the 16 zero bytes unused operand rows read
+    int ss_bytes;   // LDS bytes of the sum-of-squares partials
+};
+
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4, lgkmcnt 11:8)
+#define WAITCNT_VM_LGKM0(N) (((N) & 15) | (((N) >> 4) << 14) | (7 << 4))
+
+__device__ inline void store_kv(void *base, int kv_f16, size_t idx, float v)
+{
+    if (kv_f16) ((_Float16 *)base)[idx] = (_Float16)v;
+    else ((float *)base)[idx] = v;
+}
+
+// Sum / max over aligned groups of R lanes (R = 2, 4, 8 or 16).
+__device__ inline float group_sum(float v, int R)
+{
+    for (int o = R >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Copies `bytes` (a multiple of 16) from global memory into LDS with
+// direct-to-LDS loads, 1 KiB per wave instruction; lanes past the end are
+// masked off.
+template <int NW>
+__device__ inline void stage_dma(const void *src, uint8_t *dst, int bytes, int wid, int l)
+{
+    for (int k = wid; k * 1024 < bytes; k += NW) {
+        const int off = k * 1024 + l * 16;
+        if (off < bytes)
+            __builtin_amdgcn_global_load_lds((const gvoid_t *)((const uint8_t *)src + off),
+                                             (lvoid_t *)(dst + k * 1024), 16, 0, 0);
+    }
+}
+
+// Sum-of-squares partials [rows][stride] (count per row) packed into LDS as
+// [rows][count], 4-byte direct-to-LDS loads.
+template <int NW>
+__device__ inline void stage_ss_dma(const float *src, int stride, int count, int rows, float *dst,
+                                    int wid, int l)
+{
+    const int total = rows * count;
+    for (int k = wid; k * 64 < total; k += NW) {
+        const int f = k * 64 + l;
+        if (f < total) {
+            const int r = f / count, i = f - r * count;
+            __builtin_amdgcn_global_load_lds((const gvoid_t *)(src + (size_t)r * stride + i),
+                                             (lvoid_t *)(dst + k * 64), 4, 0, 0);
+        }
+    }
+}
+
+// Register-path copy for the chunked loop (direct-to-LDS loads issued inside
+// the k loop would make later LDS reads wait for the whole weight ring).
+template <int NW>
+__device__ inline void stage_vgpr(const uint8_t *src, uint8_t *dst, int bytes, int tid)
+{
+    constexpr int STEP = NW * 64 * 16;
+    for (int off = tid * 16; off < bytes; off += 4 * STEP) {
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int o = min(off + k * STEP, bytes - 16);
+            v[k] = *(const u32x4 *)(src + o);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (off + k * STEP < bytes) *(u32x4 *)(dst + off + k * STEP) = v[k];
+    }
+}
+
+template <int NW>
+__device__ inline void lds_zero(uint8_t *dst, int bytes, int tid)
+{
+    for (int off = tid * 16; off < bytes; off += NW * 64 * 16) *(u32x4 *)(dst + off) = u32x4{0, 0, 0, 0};
+}
+
+// Epilogue for vector v, weight row R*t + rl.  Every lane of the wave calls
+// it (shuffles within aligned groups of R lanes, one group per (vector,
+// tile)); `act` marks lanes whose (row, v) is real.
+template <int EPI>
+__device__ void epilogue(const GemvArgs &a, int t, int rl, int R, int v, bool act, float y)
+{
+#pragma clang fp contract(off)
+    const int row = t * R + rl;
+    act = act && row < a.w.rows;
+    if constexpr (EPI == EPI_STORE) {
+        if (act) a.out[(size_t)v * a.out_stride + row] = y;
+    } else if constexpr (EPI == EPI_RESID) {
+        float x = 0.0f;
+        if (act) {
+            x = a.out[(size_t)v * a.out_stride + row] + y;
+            a.out[(size_t)v * a.out_stride + row] = x;
+            if (a.next.q) act_put(a.next, v, row, x);
+        }
+        const float ss = group_sum(x * x, R);
+        if (act && rl == 0 && a.next.ss) a.next.ss[(size_t)v * a.next.ss_stride + t] = ss;
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        const float u = __shfl_xor(y, 1, 64);
+        if (act && !(row & 1)) {
+            const float h = (y / (1.0f + expf(-y))) * u;
+            if (a.out) a.out[(size_t)v * a.out_stride + (row >> 1)] = h;
+            if (a.next.q) act_put(a.next, v, row >> 1, h);
+        }
+    } else if constexpr (EPI == EPI_QKV) {
+        const float partner = __shfl_xor(y, 1, 64);
+        if (act) {
+            const int pos = min(max(a.pos[(size_t)v * a.pos_stride], 0), a.max_ctx - 1);
+            if (row < a.nq + a.nkv) {
+                const int rr = row < a.nq ? row : row - a.nq;
+                const int i = rr % a.d_head;
+                float val = y;
+                if (a.rope_on) {
+                    const float *cs = a.rope + ((size_t)pos * (a.d_head / 2) + (i >> 1)) * 2;
+                    const float c = cs[0], sn = cs[1];
+                    if (!(i & 1)) val = y * c - partner * sn;
+                    else val = partner * sn + y * c;
+                }
+                if (row < a.nq) {
+                    a.out[(size_t)v * a.out_stride + row] = val;
+                } else {
+                    const int h = rr / a.d_head;
+                    store_kv(a.kv.k_base, a.kv_f16,
+                             kv_offset(a.kv, v) + ((size_t)h * a.max_ctx + pos) * a.d_head + i, val);
+                }
+            } else {
+                const int rr = row - a.nq - a.nkv;
+                const int h = rr / a.d_head, i = rr % a.d_head;
+                store_kv(a.kv.v_base, a.kv_f16,
+                         kv_offset(a.kv, v) + ((size_t)h * a.max_ctx + pos) * a.d_head + i, y);
+            }
+        }
+    } else if constexpr (EPI == EPI_LOGITS) {
+        if (act) a.out[(size_t)v * a.out_stride + row] = y;
+        unsigned long long key = act ? argmax_key(y, (uint32_t)row) : 0ull;
+        for (int o = R >> 1; o > 0; o >>= 1) {
+            const unsigned long long other = __shfl_xor(key, o, 64);
+            key = other > key ? other : key;
+        }
+        if (act && rl == 0)
+            atomicMax(a.argmax + (size_t)v * ARGMAX_SLOTS + (t & (ARGMAX_SLOTS - 1)), key);
+    }
+}
+
+// One work-group per row tile (16 MFMA columns: R = 16/F rows x F k parts).
+// The activation operand of the whole k range is copied into LDS with
+// direct-to-LDS loads issued before the weights (in chunks only when it
+// exceeds the LDS budget); the NW waves split every k part into runs of qpc
+// quads, and each wave streams its weight quads through a ring of U
+// in-flight loads (one coalesced 16/32-byte load per lane per quad).
+//
+// MFMA A rows: row 2(vF + p) + h is the high (h = 0) or scaled low (h = 1)
+// f16 part of vector v restricted to k part p; column c of the tile holds
+// part c / R, so only the entries with matching parts are used.  Each wave
+// combines its high/low pairs and leaves the useful entries in LDS, where one
+// thread per (vector, row) sums them over waves and parts in a fixed order.
+template <int DT, int NW, int NG, bool CHUNKED, int U>
+__global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
+{
+    constexpr int LB = QFmt<DT>::LANE_BYTES;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t *s_op = smem;
+    float *s_ss = (float *)(smem + sh.op_bytes);
+    float *s_nrm = (float *)(smem + sh.op_bytes + sh.ss_bytes);
+
+    const int BQ = a.w.block_quads, F = a.w.fold, R = 16 / F;
+    const int t = blockIdx.x;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+    const int n = a.n;
+    const int vb = 128 * n;              // operand bytes per block
+    const int nblk = a.w.cols >> 5;
+    const int qpc = sh.qpc, cq = NW * qpc;
+    const int nchunks = CHUNKED ? (BQ + cq - 1) / cq : 1;
+    const int len = nchunks * qpc;
+    const size_t cell0 = (size_t)t * BQ;
+
+    // ---- 1. operand and norm partials into LDS (issued first) ----
+    if constexpr (!CHUNKED) stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
+    if (a.in.ss) stage_ss_dma<NW>(a.in.ss, a.in.ss_stride, a.in.ss_count, n, s_ss, wid, l);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. weight ring: slot u holds sequence element i with i % U == u;
+    // elements past the wave's run re-read its last quad so every slot is
+    // loaded unconditionally and the load counters stay exact ----
+    u32x4 c0[U], c1[U];
+    u32x2 dv[U];
+    uint32_t hv[U];
+    auto quad_of = [&](int i) {
+        i = min(i, len - 1);
+        const int c = CHUNKED ? i / qpc : 0;
+        return min(c * cq + wid * qpc + (i - c * qpc), BQ - 1);
+    };
+    auto load_slot = [&](int u, int i) {
+        const size_t cell = cell0 + quad_of(i);
+        const u32x4 *p = (const u32x4 *)(a.w.qs + (cell * 64 + l) * LB);
+        c0[u] = p[0];
+        if constexpr (LB == 32) c1[u] = p[1];
+        else c1[u] = u32x4{0, 0, 0, 0};
+        dv[u] = *(const u32x2 *)(a.w.d + cell * 64 + (l & 15) * 4);
+        if constexpr (DT == DT_Q5_0) hv[u] = a.w.qh[cell * 64 + l];
+        else hv[u] = 0u;
+    };
+#pragma unroll
+    for (int u = 0; u < U; u++) load_slot(u, u);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. zero padding blocks and the zero slot, then wait for the copies
+    // (loads retire in issue order: every load but the ring's) and meet ----
+    if constexpr (!CHUNKED) lds_zero<NW>(s_op + nblk * vb, sh.zslot + 16 - nblk * vb, threadIdx.x);
+    else lds_zero<NW>(s_op + sh.zslot, 16, threadIdx.x);
+    // load instructions per ring slot: codes (1 or 2) + scales (+ fifth bits)
+    constexpr int LPS = (LB == 32 ? 2 : 1) + 1 + (DT == DT_Q5_0 ? 1 : 0);
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(LPS * U));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // A-operand row fed by this lane per group: LDS address of block 0 and
+    // per-block stride (rows beyond 2nF read the zero slot)
+    const int g = l >> 4;
+    int abase[NG], astride[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+        const int ar = 16 * gi + (l & 15);
+        const int v = ar / (2 * F), p = (ar >> 1) % F, h = ar & 1;
+        const bool ok = v < n;
+        const int p0 = CHUNKED ? 0 : p * 4 * BQ;
+        abase[gi] = ok ? p0 * vb + (g * 2 * n + 2 * v + h) * 16 : sh.zslot;
+        astride[gi] = ok ? vb : 0;
+    }
+
+    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) acc[gi] = zero4;
+
+    auto compute = [&](int u, int i) {
+        const int c = CHUNKED ? i / qpc : 0, j = i - c * qpc;
+        if (CHUNKED && j == 0) {   // next operand chunk (uniform over the work-group)
+            if (c > 0) __syncthreads();
+            const int b0 = 4 * c * cq;
+            const int nb_c = min(4 * cq, nblk - b0);
+            stage_vgpr<NW>((const uint8_t *)a.in.q + (size_t)b0 * vb, s_op, nb_c * vb, threadIdx.x);
+            lds_zero<NW>(s_op + nb_c * vb, (4 * cq - nb_c) * vb, threadIdx.x);
+            __syncthreads();
+        }
+        const int lq = wid * qpc + j;
+        if (c * cq + lq >= BQ) return;
+        const float dsc[4] = {
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] & 0xFFFFu)),
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] >> 16)),
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] & 0xFFFFu)),
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] >> 16))};
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const f16x8 xv = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
+                const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, zero4, 0, 0, 0);
+                acc[gi][0] = fmaf(dsc[bi], cc[0], acc[gi][0]);
+                acc[gi][1] = fmaf(dsc[bi], cc[1], acc[gi][1]);
+                acc[gi][2] = fmaf(dsc[bi], cc[2], acc[gi][2]);
+                acc[gi][3] = fmaf(dsc[bi], cc[3], acc[gi][3]);
+            }
+        }
+    };
+    // rounds of U: while another round follows, slot u is refilled right
+    // after use (rolling prefetch); the last round issues no loads
+    for (int i0 = 0; i0 < len; i0 += U) {
+        if (i0 + U < len) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                compute(u, i0 + u);
+                load_slot(u, i0 + u + U);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (i0 + u < len) compute(u, i0 + u);
+        }
+    }
+
+    // ---- 4. RMSNorm scale per vector from the staged partials ----
+    if (a.in.ss) {
+        for (int v = wid; v < n; v += NW) {
+            float s = 0.0f;
+            for (int i = l; i < a.in.ss_count; i += 64) s += s_ss[v * a.in.ss_count + i];
+            s = wave_sum(s);
+            if (l == 0) s_nrm[v] = 1.0f / sqrtf(s / (float)a.w.cols + a.in.eps);
+        }
+    }
+    // ---- 5. the waves' useful entries meet in LDS: lane l (column c = part
+    // p x row rl) holds, per group and component pair, the high/low parts of
+    // A row 2(vF + p') + h; the pairs with p' == p are combined and stored at
+    // s_z[w][v][rl][p] ----
+    __syncthreads();   // every wave is done with the operand area
+    float *s_z = (float *)smem;
+    {
+        const int c = l & 15, pc = c / R, rc = c % R;
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int ar = 16 * gi + 4 * (l >> 4) + 2 * q;
+                const int v = ar / (2 * F), pp = (ar >> 1) % F;
+                if (v < n && pp == pc)
+                    s_z[((wid * n + v) * R + rc) * F + pp] = acc[gi][2 * q] + acc[gi][2 * q + 1] * LO_INV_SCALE;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 6. one thread per (vector, row): sum over waves and parts in a
+    // fixed order, scale, epilogue ----
+    const int nout = n * R;
+    for (int o0 = 0; o0 < nout; o0 += NW * 64) {
+        const int o = o0 + (int)threadIdx.x;
+        const bool act = o < nout;
+        const int v = act ? o / R : 0, rl = o % R;
+        float z = 0.0f;
+        if (act) {
+            const float *zp = s_z + ((size_t)v * R + rl) * F;
+            const int wstride = n * R * F;
+            if (F == 1) {
+#pragma unroll
+                for (int w = 0; w < NW; w++) z += zp[w * wstride];
+            } else if (F == 2) {
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    const float2 e = *(const float2 *)(zp + w * wstride);
+                    z += e.x;
+                    z += e.y;
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    for (int p4 = 0; p4 < F; p4 += 4) {
+                        const float4 e = *(const float4 *)(zp + w * wstride + p4);
+                        z += e.x;
+                        z += e.y;
+                        z += e.z;
+                        z += e.w;
+                    }
+                }
+            }
+        }
+        float y = z * ACT_INV_SCALE;
+        if (a.in.ss) y *= s_nrm[v];
+        switch (sh.epi) {
+        case EPI_STORE: epilogue<EPI_STORE>(a, t, rl, R, v, act, y); break;
+        case EPI_RESID: epilogue<EPI_RESID>(a, t, rl, R, v, act, y); break;
+        case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, rl, R, v, act, y); break;
+        case EPI_QKV: epilogue<EPI_QKV>(a, t, rl, R, v, act, y); break;
+        default: epilogue<EPI_LOGITS>(a, t, rl, R, v, act, y); break;
+        }
+    }
+}
+
+static inline int pick_nw(int tiles, int quads)
+{
+    int nw = tiles < 128 ? 16 : tiles < 256 ? 8 : 4;
+    if (const char *e = getenv("CMOL_GEMV_NW")) nw = atoi(e);
+    while (nw > 1 && quads < 2 * nw) nw >>= 1;
+    return nw;
+}
+
+static inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// LDS budget of one work-group.
+#define GEMV_LDS_BUDGET (64 * 1024)
+
+// Chooses quads per wave per chunk and the LDS areas; returns the dynamic
+// LDS bytes or -1 when the operand cannot be staged (`chunked` is set when
+// it takes more than one chunk, only possible with fold 1).
+static inline int plan_gemv(const GemvArgs &a, int nw, GemvShape &sh, bool &chunked)
+{
+    const int BQ = a.w.block_quads, F = a.w.fold;
+    const int vb = 128 * a.n;
+    sh.ss_bytes = a.in.ss ? round_up(a.n * a.in.ss_count * 4, 16) : 0;
+    const int nrm = round_up(a.n * 4, 16);
+    const int red = nw * a.n * 64;   // per-wave useful entries (16 columns x n floats)
+    const int cap = GEMV_LDS_BUDGET - sh.ss_bytes - nrm - 16;
+    const long full = (long)F * 4 * BQ * vb;
+    if (full <= cap) {
+        chunked = false;
+        sh.qpc = (BQ + nw - 1) / nw;
+        sh.zslot = (int)full;
+    } else {
+        if (F != 1) return -1;
+        chunked = true;
+        sh.qpc = cap / (4 * vb * nw);
+        if (sh.qpc < 1) return -1;
+        sh.zslot = 4 * sh.qpc * nw * vb;
+    }
+    sh.op_bytes = round_up(sh.zslot + 16 > red ? sh.zslot + 16 : red, 16);
+    return sh.op_bytes + sh.ss_bytes + nrm;
+}
+
+template <int DT, int NW, int NG>
+static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
+{
+    if (epi < EPI_STORE || epi > EPI_LOGITS) return -6;
+    GemvShape sh;
+    sh.epi = epi;
+    bool chunked = false;
+    const int lds = plan_gemv(a, NW, sh, chunked);
+    if (lds < 0) return -6;
+    const dim3 grid(a.w.row_tiles), block(NW * 64);
+    // ring depth: the short ring when a wave's whole run fits it
+    constexpr int UL = (DT == DT_Q8_0) ? 6 : 8, US = UL / 2;
+    const int len = chunked ? ((a.w.block_quads + sh.qpc * NW - 1) / (sh.qpc * NW)) * sh.qpc : sh.qpc;
+    if (chunked) {
+        if (len <= US) hipLaunchKernelGGL((k_gemv<DT, NW, NG, true, US>), grid, block, lds, s, a, sh);
+        else hipLaunchKernelGGL((k_gemv<DT, NW, NG, true, UL>), grid, block, lds, s, a, sh);
+    } else {
+        if (len <= US) hipLaunchKernelGGL((k_gemv<DT, NW, NG, false, US>), grid, block, lds, s, a, sh);
+        else hipLaunchKernelGGL((k_gemv<DT, NW, NG, false, UL>), grid, block, lds, s, a, sh);
+    }
+    return 0;
+}
+
+// Widest wave count the launch heuristics allow whose LDS plan fits.
+template <int DT, int NG>
+static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
+{
+    int nw = pick_nw(a.w.row_tiles, a.w.block_quads);
+    for (;; nw >>= 1) {
+        GemvShape sh;
+        bool ch;
+        if (nw <= 1 || plan_gemv(a, nw, sh, ch) >= 0) break;
+    }
+    if (nw >= 16) return launch_cfg<DT, 16, NG>(a, epi, s);
+    if (nw >= 8) return launch_cfg<DT, 8, NG>(a, epi, s);
+    if (nw >= 4) return launch_cfg<DT, 4, NG>(a, epi, s);
+    if (nw >= 2) return launch_cfg<DT, 2, NG>(a, epi, s);
+    return launch_cfg<DT, 1, NG>(a, epi, s);
+}
+
+template <int DT>
+int launch_ng(const GemvArgs &a, int epi, hipStream_t s)
+{
+    const int rows = 2 * a.n * a.w.fold;   // MFMA A rows
+    if (rows <= 16) return launch_dt<DT, 1>(a, epi, s);
+    if (rows <= 32) return launch_dt<DT, 2>(a, epi, s);
+    if (rows <= 64) return launch_dt<DT, 4>(a, epi, s);
+    return -6;
+}

@@ -1,4 +1,4 @@
-// kernels.h — device-side tensor view and the host launchers each kernel
+// kernels.h — device-side tensor views and the host launchers each kernel
 // translation unit exports to the C-ABI layer (cmol_hip.hip).
 #pragma once
 
@@ -10,7 +10,7 @@ struct QTensor {
     uint8_t *qs;
     uint16_t *d;
     uint32_t *qh;
-    int dtype, rows, cols, row_tiles, block_quads;
+    int dtype, rows, cols, row_tiles, block_quads, fold;
 };
 
 // KV caches of one layer for a batch of activation vectors: vector n uses
@@ -27,14 +27,56 @@ __device__ inline size_t kv_offset(const KVRef &r, int n)
     return (size_t)r.slot_ids[n] * r.slot_stride + r.layer_off;
 }
 
+// ---------------------------------------------------------------------------
+// Activation operands.
+//
+// A matvec consumes its activation vectors already in MFMA A-operand form:
+// for block b (32 inputs), k-group g (0..3) and operand row r the 8 halves
+// q[((b*4 + g)*nrows + r)*8 + e] hold input 32b + kmap(dt, g, e), where
+// operand row 2n is the f16 rounding hi of t = vector n times ACT_SCALE and
+// row 2n+1 the f16 rounding of the remainder (t - hi) times LO_SCALE.  The
+// two rows land in separate MFMA result rows, so the consumer forms
+// (hi + lo / LO_SCALE) / ACT_SCALE with exact power-of-two factors: 22
+// significant bits for |x| in [2^-6, 2^24), an absolute error below 2^-28
+// under that, and exact products with the integer codes.  When the
+// consumer starts with an RMSNorm the producer stores w (.) x instead of x
+// and per-tile sums of x^2; the consumer applies 1/sqrt(mean + eps) in its
+// epilogue (the matvec is linear).  Producers of these operands: the
+// embedding gather, residual-add / SwiGLU epilogues, attention, and
+// k_act_prep for standalone calls.
+// ---------------------------------------------------------------------------
+#define ACT_SCALE (1.0f / 256.0f)
+#define ACT_INV_SCALE 256.0f
+#define LO_SCALE 2048.0f
+#define LO_INV_SCALE (1.0f / 2048.0f)
+
+struct ActOut {
+    _Float16 *q;            // operand buffer of the consumer
+    int dt;                 // consumer weight format (selects kmap)
+    int nrows;              // 2 * vectors
+    const float *norm_w;    // consumer RMSNorm weights, or nullptr
+    float *ss;              // sum-of-squares partials [vector][ss_stride]
+    int ss_stride;
+};
+
+struct ActIn {
+    const _Float16 *q;      // operand buffer (layout above)
+    int nrows;              // 2 * vectors
+    const float *ss;        // partials [vector][ss_stride] or nullptr (no norm)
+    int ss_count, ss_stride;
+    float eps;
+};
+
 // ---- qtensor.hip
-// Repack `rows` raw GGUF rows into destination rows row0.. (concat) or
-// 2*(row0+i)+part (interleave).
+// Repack `rows` raw GGUF rows into destination rows row0.. (concat, mode 0)
+// or 2*(row0+i)+part (interleave, mode 1).
 int launch_repack(const QTensor &t, const uint8_t *raw, int rows, int row0,
                   int mode, int part, hipStream_t s);
 int launch_dequant(const QTensor &t, float *out, hipStream_t s);
+// Embedding rows of n vectors -> x (fp32) and the first consumer's operand.
 int launch_embed(const QTensor &t, const int32_t *token, int token_stride, float *x,
-                 int x_stride, unsigned long long *argmax, int n, hipStream_t s);
+                 int x_stride, const ActOut &o, unsigned long long *argmax, int n,
+                 hipStream_t s);
 
 // ---- gemv.hip
 // The LM-head argmax of one vector is spread over this many 64-bit slots
@@ -43,25 +85,23 @@ int launch_embed(const QTensor &t, const int32_t *token, int token_stride, float
 
 enum GemvEpilogue {
     EPI_STORE = 0,   // out[n][row] = y
-    EPI_RESID = 1,   // out[n][row] += y
-    EPI_SWIGLU = 2,  // rows interleaved gate/up: out[n][row/2] = silu(g)*u
-    EPI_QKV = 3,     // q rows -> q_out (RoPE), k/v rows -> KV cache at pos
+    EPI_RESID = 1,   // out[n][row] += y, then the next consumer's operand
+    EPI_SWIGLU = 2,  // rows interleaved gate/up: silu(g)*u -> operand (+ out)
+    EPI_QKV = 3,     // q rows -> out (RoPE), k/v rows -> KV cache at pos
     EPI_LOGITS = 4,  // out[n][row] = y and argmax over rows
 };
 
 struct GemvArgs {
     QTensor w;
-    const float *x;         // activations [n][x_stride]
-    int x_stride;
-    const float *norm_w;    // RMSNorm weights [cols] or nullptr
-    float eps;
+    ActIn in;
     float *out;             // epilogue output [n][out_stride]
     int out_stride;
-    int n;                  // activation vectors (sessions)
+    int n;                  // activation vectors
+    ActOut next;            // EPI_RESID / EPI_SWIGLU: operand of the consumer
     // EPI_QKV
     int nq, nkv, d_head, max_ctx, kv_f16, rope_on;
     const float *rope;      // [max_ctx][d_head/2][2]
-    KVRef kv;               // caches of this layer (layout [n_kv][max_ctx][d_head])
+    KVRef kv;
     const int32_t *pos;     // per-vector position, pos[n * pos_stride]
     int pos_stride;
     // EPI_LOGITS
@@ -69,6 +109,10 @@ struct GemvArgs {
 };
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);
+// x [n][x_stride] fp32 -> operand (and sum-of-squares partials per 32 inputs).
+int launch_act_prep(const float *x, int x_stride, int K, int n, const ActOut &o, hipStream_t s);
+// Operand bytes for K inputs (padded to whole block quads) and n vectors.
+size_t act_bytes(int K, int n);
 
 // ---- attn.hip
 struct AttnArgs {
@@ -81,18 +125,41 @@ struct AttnArgs {
     int split;              // positions per work-group
     int max_splits;
     float *pm, *pl, *po;    // partials [n][n_kv][max_splits][G]( [d_head])
-    float *out;             // [n][out_stride]
+    float *out;             // [n][out_stride] fp32, or nullptr
     int out_stride;
+    ActOut next;            // operand of the output projection (q == nullptr: none)
 };
 
 int launch_attn(const AttnArgs &a, hipStream_t s);
 int attn_max_splits(int max_ctx, int split);
 
 // ---- misc.hip
-int launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 int launch_kv_synth(void *kc, void *vc, int n_kv, int max_ctx, int d_head,
                     int n_tokens, int kv_f16, uint64_t seed, hipStream_t s);
 int launch_kv_convert(const void *src, float *dst, int n_kv, int max_ctx,
                       int d_head, int n, int kv_f16, int to_ref, hipStream_t s);
 int launch_kv_import(const float *src, void *dst, int n_kv, int max_ctx,
                      int d_head, int n, int kv_f16, hipStream_t s);
+
+// Writes value v of input k of vector n into an operand (see ActOut).
+__device__ inline void act_put(const ActOut &o, int n, int k, float v)
+{
+#pragma clang fp contract(off)
+    const float t = (o.norm_w ? o.norm_w[k] * v : v) * ACT_SCALE;
+    const _Float16 hi = (_Float16)t;
+    const _Float16 lo = (_Float16)((t - (float)hi) * LO_SCALE);
+    const int b = k >> 5, kk = k & 31;
+    int g, e;
+    if (o.dt == 8) {
+        g = kk >> 3;
+        e = kk & 7;
+    } else {
+        const int hi16 = kk >> 4, r = kk & 15;   // kmap inverse for the nibble order
+        g = r >> 2;
+        const int j = r & 3;
+        e = hi16 * 4 + (j == 1 ? 2 : j == 2 ? 1 : j);
+    }
+    const size_t base = (((size_t)b * 4 + g) * o.nrows + 2 * n) * 8 + e;
+    o.q[base] = hi;
+    o.q[base + 8] = lo;
+}

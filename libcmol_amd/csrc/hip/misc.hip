@@ -2,21 +2,6 @@
 #include "common.h"
 #include "kernels.h"
 
-__global__ void k_fill_f32(float *p, size_t n, float v)
-{
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
-}
-
-int launch_fill_f32(float *p, size_t n, float v, hipStream_t s)
-{
-    if (!n) return 0;
-    unsigned grid = (unsigned)((n + 255) / 256);
-    if (grid > 65535u * 16u) grid = 65535u * 16u;
-    hipLaunchKernelGGL(k_fill_f32, dim3(grid), dim3(256), 0, s, p, n, v);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
 __device__ inline uint64_t mix64d(uint64_t z)
 {
     z += 0x9E3779B97F4A7C15ull;

@@ -3,128 +3,104 @@
 #include "common.h"
 #include "kernels.h"
 
-// One thread per (tile, quad, lane): gathers the lane's codes for 4 blocks,
-// its Q5_0 fifth-bit byte per block, and (lanes 0..15) the row's 4 scales.
-template <int DT>
-__global__ void k_repack(const uint8_t *__restrict__ raw, int rows, int nb,
-                         int row0, int BQ, uint8_t *__restrict__ qs,
-                         uint16_t *__restrict__ dsc, uint32_t *__restrict__ qh,
-                         int tile0, int tiles)
+// Position of a destination tensor element in the tiled layout.
+struct CellPos {
+    size_t cell;   // t * BQ + q
+    int col;       // MFMA column 0..15
+    int bi;        // block within the quad
+};
+
+__device__ inline CellPos cell_pos(const QTensor &t, int row, int b)
 {
-    constexpr int LB = QFmt<DT>::LANE_BYTES, BB = QFmt<DT>::BLOCK_BYTES;
-    long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    long total = (long)tiles * BQ * 64;
-    if (gid >= total) return;
-    int lane = (int)(gid & 63);
-    long cell = (gid >> 6) + (long)tile0 * BQ;   // t * BQ + q
-    int q = (int)(cell % BQ);
-    int t = (int)(cell / BQ);
-    int r16 = lane & 15, g = lane >> 4;
-    int grow = t * 16 + r16;            // row within the destination tensor
-    int srow = grow - row0;             // row within this part
-    uint8_t out[LB];
-    uint32_t hword = 0;
-    uint16_t dv[4];
-    for (int bi = 0; bi < 4; bi++) {
-        int b = q * 4 + bi;
-        bool valid = srow >= 0 && srow < rows && b < nb;
-        const uint8_t *src = raw + ((size_t)(valid ? srow : 0) * nb + (valid ? b : 0)) * BB;
-        dv[bi] = valid ? (uint16_t)(src[0] | (src[1] << 8)) : 0;
-        if constexpr (DT == DT_Q8_0) {
-            for (int j = 0; j < 8; j++) out[bi * 8 + j] = valid ? src[2 + 8 * g + j] : 0;
-        } else if constexpr (DT == DT_Q4_0) {
-            for (int j = 0; j < 4; j++) out[bi * 4 + j] = valid ? src[2 + 4 * g + j] : 0;
-        } else {
-            for (int j = 0; j < 4; j++) out[bi * 4 + j] = valid ? src[6 + 4 * g + j] : 0;
-            uint32_t qhw = valid ? (uint32_t)src[2] | ((uint32_t)src[3] << 8) |
-                                   ((uint32_t)src[4] << 16) | ((uint32_t)src[5] << 24)
-                                 : 0u;
-            // byte layout expected by deq_q5: bit p = fifth bit of pair p's
-            // low element, bit 4+p = fifth bit of its high element
-            int base = 4 * g;
-            uint32_t hb = 0;
-            hb |= ((qhw >> (base + 0)) & 1u) << 0;        // p0 lo: lo(b0)
-            hb |= ((qhw >> (base + 2)) & 1u) << 4;        // p0 hi: lo(b2)
-            hb |= ((qhw >> (base + 1)) & 1u) << 1;        // p1 lo: lo(b1)
-            hb |= ((qhw >> (base + 3)) & 1u) << 5;        // p1 hi: lo(b3)
-            hb |= ((qhw >> (16 + base + 0)) & 1u) << 2;   // p2 lo: hi(b0)
-            hb |= ((qhw >> (16 + base + 2)) & 1u) << 6;   // p2 hi: hi(b2)
-            hb |= ((qhw >> (16 + base + 1)) & 1u) << 3;   // p3 lo: hi(b1)
-            hb |= ((qhw >> (16 + base + 3)) & 1u) << 7;   // p3 hi: hi(b3)
-            hword |= hb << (8 * bi);
-        }
-    }
-    // Only rows of this part are written; the tensor is zero-filled before
-    // the first part, which covers padding rows beyond every part.
-    if (srow < 0 || srow >= rows) return;
-    uint8_t *dst = qs + ((size_t)cell * 64 + lane) * LB;
-    for (int j = 0; j < LB; j += 4)
-        *(uint32_t *)(dst + j) = (uint32_t)out[j] | ((uint32_t)out[j + 1] << 8) |
-                                 ((uint32_t)out[j + 2] << 16) | ((uint32_t)out[j + 3] << 24);
-    if constexpr (DT == DT_Q5_0) qh[(size_t)cell * 64 + lane] = hword;
-    if (g == 0) {
-        uint16_t *dd = dsc + (size_t)cell * 64 + r16 * 4;
-        for (int bi = 0; bi < 4; bi++) dd[bi] = dv[bi];
+    const int R = 16 / t.fold, BQ = t.block_quads;
+    const int part = b / (4 * BQ), bq = b - part * 4 * BQ;
+    CellPos p;
+    p.cell = (size_t)(row / R) * BQ + (bq >> 2);
+    p.col = part * R + row % R;
+    p.bi = bq & 3;
+    return p;
+}
+
+// The lane's share of one GGUF block: codes (LB/4 bytes) and, for Q5_0, the
+// byte of fifth bits in the pair order deq_q5 expects (bit p = fifth bit of
+// pair p's low element, bit 4+p = of its high element).
+template <int DT>
+__device__ inline void lane_block(const uint8_t *src, int g, uint8_t *out, uint32_t *hb)
+{
+    if constexpr (DT == DT_Q8_0) {
+        for (int j = 0; j < 8; j++) out[j] = src[2 + 8 * g + j];
+        *hb = 0;
+    } else if constexpr (DT == DT_Q4_0) {
+        for (int j = 0; j < 4; j++) out[j] = src[2 + 4 * g + j];
+        *hb = 0;
+    } else {
+        for (int j = 0; j < 4; j++) out[j] = src[6 + 4 * g + j];
+        const uint32_t qhw = (uint32_t)src[2] | ((uint32_t)src[3] << 8) |
+                             ((uint32_t)src[4] << 16) | ((uint32_t)src[5] << 24);
+        const int base = 4 * g;
+        uint32_t h = 0;
+        h |= ((qhw >> (base + 0)) & 1u) << 0;        // p0 lo: lo(b0)
+        h |= ((qhw >> (base + 2)) & 1u) << 4;        // p0 hi: lo(b2)
+        h |= ((qhw >> (base + 1)) & 1u) << 1;        // p1 lo: lo(b1)
+        h |= ((qhw >> (base + 3)) & 1u) << 5;        // p1 hi: lo(b3)
+        h |= ((qhw >> (16 + base + 0)) & 1u) << 2;   // p2 lo: hi(b0)
+        h |= ((qhw >> (16 + base + 2)) & 1u) << 6;   // p2 hi: hi(b2)
+        h |= ((qhw >> (16 + base + 1)) & 1u) << 3;   // p3 lo: hi(b1)
+        h |= ((qhw >> (16 + base + 3)) & 1u) << 7;   // p3 hi: hi(b3)
+        *hb = h;
     }
 }
 
-// Interleave mode: destination row 2i+p comes from part p row i.
+// One thread per (tile, quad, lane) of the destination tiles a chunk of
+// source rows lands in.  Source row i of the chunk is destination row
+// row0 + i (concat) or 2*(row0 + i) + part (interleave).  Lanes whose row
+// belongs to another chunk are left alone (the tensor is zero-filled first,
+// which also covers padding rows and blocks).
 template <int DT>
-__global__ void k_repack_il(const uint8_t *__restrict__ raw, int rows, int nb,
-                            int row0, int part, int BQ, uint8_t *__restrict__ qs,
-                            uint16_t *__restrict__ dsc, uint32_t *__restrict__ qh,
-                            int tile0, int tiles)
+__global__ void k_repack(const uint8_t *__restrict__ raw, int rows, int row0, int mode,
+                         int part, QTensor t, int tile0, int tiles)
 {
     constexpr int LB = QFmt<DT>::LANE_BYTES, BB = QFmt<DT>::BLOCK_BYTES;
-    long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    long total = (long)tiles * BQ * 64;
-    if (gid >= total) return;
-    int lane = (int)(gid & 63);
-    long cell = (gid >> 6) + (long)tile0 * BQ;
-    int q = (int)(cell % BQ);
-    int t = (int)(cell / BQ);
-    int r16 = lane & 15, g = lane >> 4;
-    int grow = t * 16 + r16;
-    if ((grow & 1) != part) return;
-    int srow = (grow >> 1) - row0;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int BQ = t.block_quads, R = 16 / t.fold, nb = t.cols / 32;
+    if (gid >= (long)tiles * BQ * 64) return;
+    const int lane = (int)(gid & 63);
+    const long cell = (gid >> 6) + (long)tile0 * BQ;
+    const int q = (int)(cell % BQ), tt = (int)(cell / BQ);
+    const int c = lane & 15, g = lane >> 4;
+    const int drow = tt * R + c % R;
+    const int kpart = c / R;
+    int srow;
+    if (mode == 0) {
+        srow = drow - row0;
+    } else {
+        if ((drow & 1) != part) return;
+        srow = (drow >> 1) - row0;
+    }
     if (srow < 0 || srow >= rows) return;
     uint8_t out[LB];
     uint32_t hword = 0;
     uint16_t dv[4];
     for (int bi = 0; bi < 4; bi++) {
-        int b = q * 4 + bi;
-        bool valid = b < nb;
-        const uint8_t *src = raw + ((size_t)srow * nb + (valid ? b : 0)) * BB;
-        dv[bi] = valid ? (uint16_t)(src[0] | (src[1] << 8)) : 0;
-        if constexpr (DT == DT_Q8_0) {
-            for (int j = 0; j < 8; j++) out[bi * 8 + j] = valid ? src[2 + 8 * g + j] : 0;
-        } else if constexpr (DT == DT_Q4_0) {
-            for (int j = 0; j < 4; j++) out[bi * 4 + j] = valid ? src[2 + 4 * g + j] : 0;
-        } else {
-            for (int j = 0; j < 4; j++) out[bi * 4 + j] = valid ? src[6 + 4 * g + j] : 0;
-            uint32_t qhw = valid ? (uint32_t)src[2] | ((uint32_t)src[3] << 8) |
-                                   ((uint32_t)src[4] << 16) | ((uint32_t)src[5] << 24)
-                                 : 0u;
-            int base = 4 * g;
-            uint32_t hb = 0;
-            hb |= ((qhw >> (base + 0)) & 1u) << 0;
-            hb |= ((qhw >> (base + 2)) & 1u) << 4;
-            hb |= ((qhw >> (base + 1)) & 1u) << 1;
-            hb |= ((qhw >> (base + 3)) & 1u) << 5;
-            hb |= ((qhw >> (16 + base + 0)) & 1u) << 2;
-            hb |= ((qhw >> (16 + base + 2)) & 1u) << 6;
-            hb |= ((qhw >> (16 + base + 1)) & 1u) << 3;
-            hb |= ((qhw >> (16 + base + 3)) & 1u) << 7;
+        const int b = kpart * 4 * BQ + q * 4 + bi;
+        if (b < nb) {
+            const uint8_t *src = raw + ((size_t)srow * nb + b) * BB;
+            uint32_t hb;
+            lane_block<DT>(src, g, out + bi * (LB / 4), &hb);
             hword |= hb << (8 * bi);
+            dv[bi] = (uint16_t)(src[0] | (src[1] << 8));
+        } else {
+            for (int j = 0; j < LB / 4; j++) out[bi * (LB / 4) + j] = 0;
+            dv[bi] = 0;
         }
     }
-    uint8_t *dst = qs + ((size_t)cell * 64 + lane) * LB;
+    uint8_t *dst = t.qs + ((size_t)cell * 64 + lane) * LB;
     for (int j = 0; j < LB; j += 4)
         *(uint32_t *)(dst + j) = (uint32_t)out[j] | ((uint32_t)out[j + 1] << 8) |
                                  ((uint32_t)out[j + 2] << 16) | ((uint32_t)out[j + 3] << 24);
-    if constexpr (DT == DT_Q5_0) qh[(size_t)cell * 64 + lane] = hword;
+    if constexpr (DT == DT_Q5_0) t.qh[(size_t)cell * 64 + lane] = hword;
     if (g == 0) {
-        uint16_t *dd = dsc + (size_t)cell * 64 + r16 * 4;
+        uint16_t *dd = t.d + (size_t)cell * 64 + c * 4;
         for (int bi = 0; bi < 4; bi++) dd[bi] = dv[bi];
     }
 }
@@ -133,21 +109,14 @@ int launch_repack(const QTensor &t, const uint8_t *raw, int rows, int row0,
                   int mode, int part, hipStream_t s)
 {
     if (rows <= 0) return 0;
-    int d0 = mode == 0 ? row0 : 2 * row0 + part;
-    int d1 = mode == 0 ? row0 + rows - 1 : 2 * (row0 + rows - 1) + part;
-    int tile0 = d0 / 16, tiles = d1 / 16 - tile0 + 1;
+    const int R = 16 / t.fold;
+    const int d0 = mode == 0 ? row0 : 2 * row0 + part;
+    const int d1 = mode == 0 ? row0 + rows - 1 : 2 * (row0 + rows - 1) + part;
+    const int tile0 = d0 / R, tiles = d1 / R - tile0 + 1;
     if (tile0 < 0 || tile0 + tiles > t.row_tiles) return -6;
-    long total = (long)tiles * t.block_quads * 64;
-    int threads = 256;
-    unsigned grid = (unsigned)((total + threads - 1) / threads);
-    int nb = t.cols / 32;
-#define REPACK(DTV)                                                                       \
-    if (mode == 0)                                                                        \
-        hipLaunchKernelGGL(k_repack<DTV>, dim3(grid), dim3(threads), 0, s, raw, rows, nb, \
-                           row0, t.block_quads, t.qs, t.d, t.qh, tile0, tiles);            \
-    else                                                                                  \
-        hipLaunchKernelGGL(k_repack_il<DTV>, dim3(grid), dim3(threads), 0, s, raw, rows,  \
-                           nb, row0, part, t.block_quads, t.qs, t.d, t.qh, tile0, tiles);
+    const long total = (long)tiles * t.block_quads * 64;
+    const unsigned grid = (unsigned)((total + 255) / 256);
+#define REPACK(DTV) hipLaunchKernelGGL(k_repack<DTV>, dim3(grid), dim3(256), 0, s, raw, rows, row0, mode, part, t, tile0, tiles)
     switch (t.dtype) {
     case DT_Q4_0: REPACK(DT_Q4_0); break;
     case DT_Q5_0: REPACK(DT_Q5_0); break;
@@ -158,24 +127,27 @@ int launch_repack(const QTensor &t, const uint8_t *raw, int rows, int row0,
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-// Decoded value of one block: 32 floats in natural k order, computed through
-// the same lane decoders the GEMM uses, times the fp32 scale.
+// Decoded values of lane group g of one block (8 floats, written at their
+// natural k positions), computed through the same lane decoders the matvec
+// uses, times the fp32 scale.
 template <int DT>
-__device__ void block_values(const QTensor &t, int row, int b, float *dst, int dst_stride)
+__device__ void block_values_g(const QTensor &t, int row, int b, int g, float *dst)
 {
     constexpr int LB = QFmt<DT>::LANE_BYTES;
-    int tt = row >> 4, r16 = row & 15, q = b >> 2, bi = b & 3;
-    size_t cell = (size_t)tt * t.block_quads + q;
-    float d = f16_bits_to_f32(t.d[cell * 64 + r16 * 4 + bi]);
-    for (int g = 0; g < 4; g++) {
-        int lane = g * 16 + r16;
-        const u32x4 *p = (const u32x4 *)(t.qs + (cell * 64 + lane) * LB);
-        u32x4 c0 = p[0], c1 = LB == 32 ? p[1] : u32x4{0, 0, 0, 0};
-        uint32_t h = DT == DT_Q5_0 ? t.qh[cell * 64 + lane] : 0u;
-        f16x8 v = deq_block<DT>(c0, c1, h, bi);
-        for (int e = 0; e < 8; e++)
-            dst[kmap(DT, g, e) * dst_stride] = mul_scale_x86(d, (float)v[e]);
-    }
+    const CellPos cp = cell_pos(t, row, b);
+    const float d = f16_bits_to_f32(t.d[cp.cell * 64 + cp.col * 4 + cp.bi]);
+    const int lane = g * 16 + cp.col;
+    const u32x4 *p = (const u32x4 *)(t.qs + (cp.cell * 64 + lane) * LB);
+    const u32x4 c0 = p[0], c1 = LB == 32 ? p[1] : u32x4{0, 0, 0, 0};
+    const uint32_t h = DT == DT_Q5_0 ? t.qh[cp.cell * 64 + lane] : 0u;
+    const f16x8 v = deq_block<DT>(c0, c1, h, cp.bi);
+    for (int e = 0; e < 8; e++) dst[kmap(DT, g, e)] = mul_scale_x86(d, (float)v[e]);
+}
+
+template <int DT>
+__device__ void block_values(const QTensor &t, int row, int b, float *dst)
+{
+    for (int g = 0; g < 4; g++) block_values_g<DT>(t, row, b, g, dst);
 }
 
 template <int DT>
@@ -186,7 +158,7 @@ __global__ void k_dequant(QTensor t, float *__restrict__ out)
     long total = (long)t.rows * nb;
     if (gid >= total) return;
     int row = (int)(gid / nb), b = (int)(gid % nb);
-    block_values<DT>(t, row, b, out + (size_t)row * t.cols + (size_t)b * 32, 1);
+    block_values<DT>(t, row, b, out + (size_t)row * t.cols + (size_t)b * 32);
 }
 
 int launch_dequant(const QTensor &t, float *out, hipStream_t s)
@@ -202,34 +174,51 @@ int launch_dequant(const QTensor &t, float *out, hipStream_t s)
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-// Embedding rows for n vectors: x[s][:] = dequant(row token[s]).  Thread per
-// block.  Also clears each vector's argmax slots for the LM head that ends
-// the step.
+// Embedding rows for n vectors: x[s][:] = dequant(row token[s]), plus the
+// first consumer's operand and its per-block sums of squares.  Four threads
+// per block (one per lane group).  Work-group (0, s) also clears vector s's
+// argmax slots for the LM head that ends the step.
 template <int DT>
-__global__ void k_embed(QTensor t, const int32_t *__restrict__ token, int token_stride,
-                        float *__restrict__ x, int x_stride,
-                        unsigned long long *__restrict__ argmax, int n)
+__global__ __launch_bounds__(256) void k_embed(QTensor t, const int32_t *__restrict__ token,
+                                               int token_stride, float *__restrict__ x,
+                                               int x_stride, ActOut o,
+                                               unsigned long long *__restrict__ argmax, int n)
 {
-    int s = blockIdx.y;
+#pragma clang fp contract(off)
+    const int s = blockIdx.y;
     if (s >= n) return;
-    int nb = t.cols / 32;
+    const int nb = t.cols / 32;
     int tok = token[s * token_stride];
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < ARGMAX_SLOTS; i += blockDim.x) argmax[(size_t)s * ARGMAX_SLOTS + i] = 0ull;
     if (tok < 0 || tok >= t.rows) tok = 0;
-    for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += gridDim.x * blockDim.x)
-        block_values<DT>(t, tok, b, x + (size_t)s * x_stride + (size_t)b * 32, 1);
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int b = gid >> 2, g = gid & 3;
+    float ss = 0.0f;
+    if (b < nb) {
+        float *xb = x + (size_t)s * x_stride + (size_t)b * 32;
+        block_values_g<DT>(t, tok, b, g, xb);
+        for (int e = 0; e < 8; e++) {
+            const int k = kmap(DT, g, e);
+            ss += xb[k] * xb[k];
+            if (o.q) act_put(o, s, 32 * b + k, xb[k]);
+        }
+    }
+    // per-block sum over the 4 lane groups (lanes 4b..4b+3 of the wave)
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    if (b < nb && g == 0 && o.ss) o.ss[(size_t)s * o.ss_stride + b] = ss;
 }
 
 int launch_embed(const QTensor &t, const int32_t *token, int token_stride, float *x,
-                 int x_stride, unsigned long long *argmax, int n, hipStream_t s)
+                 int x_stride, const ActOut &o, unsigned long long *argmax, int n, hipStream_t s)
 {
-    int nb = t.cols / 32;
-    dim3 grid((nb + 63) / 64, n);
+    const int nb = t.cols / 32;
+    dim3 grid((nb * 4 + 255) / 256, n);
     switch (t.dtype) {
-    case DT_Q4_0: hipLaunchKernelGGL(k_embed<DT_Q4_0>, grid, dim3(64), 0, s, t, token, token_stride, x, x_stride, argmax, n); break;
-    case DT_Q5_0: hipLaunchKernelGGL(k_embed<DT_Q5_0>, grid, dim3(64), 0, s, t, token, token_stride, x, x_stride, argmax, n); break;
-    case DT_Q8_0: hipLaunchKernelGGL(k_embed<DT_Q8_0>, grid, dim3(64), 0, s, t, token, token_stride, x, x_stride, argmax, n); break;
+    case DT_Q4_0: hipLaunchKernelGGL(k_embed<DT_Q4_0>, grid, dim3(256), 0, s, t, token, token_stride, x, x_stride, o, argmax, n); break;
+    case DT_Q5_0: hipLaunchKernelGGL(k_embed<DT_Q5_0>, grid, dim3(256), 0, s, t, token, token_stride, x, x_stride, o, argmax, n); break;
+    case DT_Q8_0: hipLaunchKernelGGL(k_embed<DT_Q8_0>, grid, dim3(256), 0, s, t, token, token_stride, x, x_stride, o, argmax, n); break;
     default: return -4;
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;

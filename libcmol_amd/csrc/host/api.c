@@ -9,7 +9,9 @@
  * (include/cmol_hip.h): weights, KV caches and activations are placed in one
  * device arena inside cmol_load; nothing is allocated after cmol_load.
  */
+#ifndef _DEFAULT_SOURCE
 #define _DEFAULT_SOURCE
+#endif
 #include "internal.h"
 #include "../../../include/cmol_ext.h"
 

@@ -3,7 +3,9 @@
  * The CPU-feature probe of the reference has no counterpart here: the
  * compute backend is the gfx950 device (cmol_hip.h).
  */
+#ifndef _DEFAULT_SOURCE
 #define _DEFAULT_SOURCE
+#endif
 #include "internal.h"
 
 #include <fcntl.h>

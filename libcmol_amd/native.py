@@ -47,7 +47,7 @@ def greedy_params(max_new: int, **kw) -> GenParams:
 
 class QTensor(C.Structure):
     _fields_ = [("qs", P), ("d", P), ("qh", P), ("dtype", I32), ("rows", I32), ("cols", I32),
-                ("row_tiles", I32), ("block_quads", I32), ("pad_", I32)]
+                ("row_tiles", I32), ("block_quads", I32), ("fold", I32)]
 
 
 # (name, restype, argtypes) of every exported entry point declared in include/*.h
@@ -78,12 +78,16 @@ SIGNATURES = [
     ("cmolhip_memcpy_d2d", C.c_int, [P, P, P, C.c_size_t]),
     ("cmolhip_synchronize", C.c_int, [P]),
     ("cmolhip_stream", P, [P]),
-    ("cmolhip_qtensor_bytes", C.c_size_t, [C.c_int, C.c_int, C.c_int]),
-    ("cmolhip_qtensor_upload", C.c_int, [P, C.c_int, C.c_int, C.c_int, C.POINTER(P),
+    ("cmolhip_qtensor_bytes", C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("cmolhip_pick_fold", C.c_int, [C.c_int, C.c_int, C.c_int]),
+    ("cmolhip_qtensor_upload", C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(P),
                                          C.POINTER(I32), C.c_int, P, C.c_size_t,
                                          C.POINTER(QTensor)]),
     ("cmolhip_dequant", C.c_int, [P, C.POINTER(QTensor), P]),
     ("cmolhip_gemm", C.c_int, [P, C.POINTER(QTensor), P, P, C.c_int, P, C.c_float]),
+    ("cmolhip_act_bytes", C.c_size_t, [C.c_int, C.c_int]),
+    ("cmolhip_act_prepare", C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P, P]),
+    ("cmolhip_gemm_prepared", C.c_int, [P, C.POINTER(QTensor), P, C.c_int, P, C.c_float, P]),
     ("cmolhip_matmul_host", C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int]),
     ("cmolhip_attn_decode", C.c_int, [P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int,
                                       C.c_int, C.c_int, P]),
@@ -188,14 +192,15 @@ class Ctx:
         return d
 
     def qtensor(self, raw_parts, dtype: int, cols: int, rows, mode: int = 0,
-                staging_bytes: int | None = None, staging: int | None = None) -> QTensor:
+                staging_bytes: int | None = None, staging: int | None = None,
+                fold: int = 1) -> QTensor:
         parts = [np.ascontiguousarray(p, np.uint8) for p in raw_parts]
         staging_bytes = staging_bytes or max(p.nbytes for p in parts)
         stg = staging if staging is not None else self.alloc(staging_bytes)
         arr_p = (C.c_void_p * len(parts))(*[p.ctypes.data for p in parts])
         arr_r = (I32 * len(parts))(*rows)
         t = QTensor()
-        check(lib().cmolhip_qtensor_upload(self.h, dtype, cols, len(parts), arr_p, arr_r, mode,
+        check(lib().cmolhip_qtensor_upload(self.h, dtype, cols, fold, len(parts), arr_p, arr_r, mode,
                                            C.c_void_p(stg), staging_bytes, C.byref(t)), "upload")
         return t
 
@@ -215,6 +220,22 @@ class Ctx:
                                  C.c_void_p(dn) if dn else None, eps), "gemm")
         check(lib().cmolhip_synchronize(self.h), "sync")
         return self.d2h(dy, (n, t.rows), np.float32)
+
+    def act_prepare(self, t: QTensor, dx: int, n: int, norm_w: int | None = None):
+        """Device operand (and sum-of-squares partials when norm_w is given)
+        for n fp32 vectors at device address dx; returns (op, ss)."""
+        op = self.alloc(lib().cmolhip_act_bytes(t.cols, n))
+        ss = self.alloc(n * (t.cols // 32) * 4) if norm_w else None
+        check(lib().cmolhip_act_prepare(self.h, C.c_void_p(dx), n, t.cols, t.dtype,
+                                        C.c_void_p(norm_w) if norm_w else None, C.c_void_p(op),
+                                        C.c_void_p(ss) if ss else None), "act_prepare")
+        return op, ss
+
+    def gemm_prepared(self, t: QTensor, op: int, n: int, ss: int | None, dy: int,
+                      eps: float = 1e-5):
+        check(lib().cmolhip_gemm_prepared(self.h, C.byref(t), C.c_void_p(op), n,
+                                          C.c_void_p(ss) if ss else None, eps, C.c_void_p(dy)),
+              "gemm_prepared")
 
     def stream(self):
         return lib().cmolhip_stream(self.h)

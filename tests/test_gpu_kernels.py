@@ -28,11 +28,13 @@ def ctx(gpu):
 
 
 @pytest.mark.parametrize("dtype", [2, 6, 8])
-@pytest.mark.parametrize("shape", [(16, 128), (37, 96), (64, 2048), (3, 4096)])
-def test_dequant_bit_exact(ctx, dtype, shape):
+@pytest.mark.parametrize("shape,fold", [((16, 128), 1), ((37, 96), 1), ((64, 2048), 1), ((3, 4096), 1),
+                                        ((37, 96), 2), ((64, 2048), 4), ((21, 1344), 8), ((5, 160), 4)])
+def test_dequant_bit_exact(ctx, dtype, shape, fold):
+    """Every fold of the tiled layout dequantises to the reference rows."""
     rows, cols = shape
     raw = random_blocks(dtype, rows, cols, seed=rows * 7 + cols + dtype)
-    t = ctx.qtensor([raw], dtype, cols, [rows])
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
     got = ctx.dequant(t)
     want = np.stack([O.dequant_row(raw[r], cols, dtype) for r in range(rows)])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -49,7 +51,8 @@ def test_dequant_special_scales_bit_exact(ctx, dtype):
 
 
 @pytest.mark.parametrize("dtype", [2, 6, 8])
-def test_upload_concat_interleave_chunked(ctx, dtype):
+@pytest.mark.parametrize("fold", [1, 4])
+def test_upload_concat_interleave_chunked(ctx, dtype, fold):
     """Row-concatenated and row-interleaved uploads, staged in small chunks,
     dequantise to the stacked / interleaved reference rows."""
     cols = 160
@@ -57,12 +60,12 @@ def test_upload_concat_interleave_chunked(ctx, dtype):
     b = random_blocks(dtype, 24, cols, seed=2)
     c = random_blocks(dtype, 24, cols, seed=3)
     bb = a.shape[1]
-    t = ctx.qtensor([a, b, c], dtype, cols, [40, 24, 24], mode=0, staging_bytes=bb * 5)
+    t = ctx.qtensor([a, b, c], dtype, cols, [40, 24, 24], mode=0, staging_bytes=bb * 5, fold=fold)
     want = np.concatenate([a, b, c])
     got = ctx.dequant(t)
     ref = np.stack([O.dequant_row(want[r], cols, dtype) for r in range(want.shape[0])])
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
-    t2 = ctx.qtensor([b, c], dtype, cols, [24, 24], mode=1, staging_bytes=bb * 7)
+    t2 = ctx.qtensor([b, c], dtype, cols, [24, 24], mode=1, staging_bytes=bb * 7, fold=fold)
     got2 = ctx.dequant(t2)
     il = np.empty((48, bb), np.uint8)
     il[0::2], il[1::2] = b, c
@@ -70,16 +73,33 @@ def test_upload_concat_interleave_chunked(ctx, dtype):
     assert np.array_equal(got2.view(np.uint32), ref2.view(np.uint32))
 
 
-@pytest.mark.parametrize("dtype,rows,cols", [
-    (8, 64, 256), (6, 48, 960), (2, 96, 576), (8, 49152 // 16, 576), (2, 320, 2560),
-    (2, 11008, 2048), (2, 2048, 11008), (8, 1024, 2048), (6, 2560, 960)])
-def test_gemv_matches_oracle(ctx, dtype, rows, cols):
+@pytest.mark.parametrize("dtype,rows,cols,fold", [
+    (8, 64, 256, 1), (6, 48, 960, 1), (2, 96, 576, 1), (8, 49152 // 16, 576, 1), (2, 320, 2560, 1),
+    (2, 11008, 2048, 1), (2, 2048, 11008, 1), (8, 1024, 2048, 1), (6, 2560, 960, 1),
+    (2, 2048, 2048, 4), (2, 2048, 11008, 4), (2, 3072, 2048, 4), (8, 576, 576, 8),
+    (6, 960, 960, 2), (2, 130, 4096, 8)])
+def test_gemv_matches_oracle(ctx, dtype, rows, cols, fold):
     raw = random_blocks(dtype, rows, cols, seed=rows + cols + dtype)
     x = np.random.default_rng(5).standard_normal(cols).astype(np.float32)
-    t = ctx.qtensor([raw], dtype, cols, [rows])
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
     got = ctx.gemm(t, x)[0]
     want = O.matmul(raw, x, rows, cols, dtype, O.AVX512)[:, 0]
-    assert_close(got, want, f"gemv q{dtype} {rows}x{cols}")
+    assert_close(got, want, f"gemv q{dtype} {rows}x{cols} fold {fold}")
+
+
+@pytest.mark.parametrize("dtype,rows,cols,fold,n", [
+    (2, 256, 2048, 1, 3), (2, 256, 2048, 1, 8), (2, 128, 11008, 1, 8), (2, 200, 2048, 1, 17),
+    (8, 96, 960, 1, 32), (6, 160, 2560, 1, 16), (2, 512, 2048, 4, 2), (2, 512, 2048, 4, 4),
+    (2, 64, 2048, 2, 4), (8, 48, 576, 8, 2)])
+def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
+    """Several activation vectors per launch (multi-session decode), including
+    operands staged in chunks (n * cols too large for one LDS copy)."""
+    raw = random_blocks(dtype, rows, cols, seed=rows * 3 + cols + n)
+    x = np.random.default_rng(n).standard_normal((n, cols)).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
+    got = ctx.gemm(t, x)
+    want = O.matmul(raw, np.ascontiguousarray(x.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"gemm q{dtype} {rows}x{cols} fold {fold} n {n}")
 
 
 def test_gemv_rmsnorm_prologue(ctx):
