@@ -48,9 +48,10 @@ def q4_bytes(m, k, n):
 
 def bench_matvec(rows, cols, n, copies, launches):
     """Average duration of the Q4_0 matvec kernel over `copies` distinct
-    weight buffers (defeating the 256 MB Infinity Cache), each launch
-    bracketed by its own HIP events on the context stream.  The weights use
-    the fold a model serving n sessions gives this shape."""
+    weight buffers (defeating the 256 MB Infinity Cache): every launch records
+    a pair of HIP events at the kernel's own start and end (on the stream it
+    runs on).  The weights use the fold a model serving n sessions gives this
+    shape."""
     fold = native.lib().cmolhip_pick_fold(rows, cols, n)
     w = synth.normal(rows * cols, seed=1234, stream=rows * 7 + cols, std=0.02)
     raw = synth.quantize(synth.Q4_0, w).reshape(rows, -1)
@@ -66,18 +67,18 @@ def bench_matvec(rows, cols, n, copies, launches):
     op, _ = ctx.act_prepare(ts[0], dx, n)
     L = native.lib()
 
-    def launch(i):
-        native.check(L.cmolhip_gemm_prepared(ctx.h, C.byref(ts[i % copies]), C.c_void_p(op), n,
-                                             None, 0.0, C.c_void_p(dy)), "gemm_prepared")
+    def launch(i, ev=None):
+        native.check(L.cmolhip_gemm_prepared_timed(
+            ctx.h, C.byref(ts[i % copies]), C.c_void_p(op), n, None, 0.0, C.c_void_p(dy),
+            ev.a if ev else None, ev.b if ev else None), "gemm_prepared")
 
     for i in range(min(copies, 8)):
         launch(i)
     native.check(L.cmolhip_synchronize(ctx.h))
+    # events recorded by each launch at the kernel's own start and end
     evs = [hiprt.EventTimer(ctx.stream()) for _ in range(launches)]
     for i, ev in enumerate(evs):
-        ev.start()
-        launch(i)
-        ev.stop()
+        launch(i, ev)
     native.check(L.cmolhip_synchronize(ctx.h))
     per_launch_s = sum(ev.elapsed() for ev in evs) / 1e3 / launches
     for ev in evs:
@@ -147,6 +148,20 @@ def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
             "kv_bytes_per_step": kv_bytes}
 
 
+def copy_calibration(mb, reps=4):
+    """Device-to-device copies of a known size: under a counter run their
+    read/write byte counters give the scale factor for FETCH_SIZE/WRITE_SIZE."""
+    nbytes = mb << 20
+    ctx = native.Ctx(2 * nbytes + (1 << 20))
+    a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    L = native.lib()
+    for _ in range(reps):
+        native.check(L.cmolhip_memcpy_d2d(ctx.h, C.c_void_p(b), C.c_void_p(a), nbytes), "d2d")
+    native.check(L.cmolhip_synchronize(ctx.h))
+    ctx.close()
+    return {"copy_bytes": nbytes, "copies": reps}
+
+
 def cpu_baseline(path, spec, n_tokens):
     """The oracle (reference arithmetic restated in C), one thread, decoding
     n_tokens positions of the same model."""
@@ -174,7 +189,9 @@ def main():
     ap.add_argument("--sessions", type=int, default=32)
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
-    ap.add_argument("--skip", default="", help="comma list of: multi,matvec,cpu")
+    ap.add_argument("--skip", default="", help="comma list of: decode,multi,matvec,cpu")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run device-to-device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -189,9 +206,13 @@ def main():
     path = synth.model_file(spec)
     log(f"model file ready in {time.perf_counter() - t0:.1f}s: {path}")
 
-    log("single-session decode")
-    d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup)
-    log(json.dumps(d1))
+    d1 = None
+    if "decode" not in skip:
+        log("single-session decode")
+        d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup)
+        log(json.dumps(d1))
+    if args.copy_mb:
+        log(json.dumps(copy_calibration(args.copy_mb)))
     mv = []
     if "matvec" not in skip:
         for rows, cols in ((11008, 2048), (2048, 11008)):
@@ -219,6 +240,9 @@ def main():
                 "kernel": "k_gemv<Q4_0> 11008x2048 n=1",
                 "bytes_per_launch": r["bytes_per_launch"],
                 "us_per_launch": round(r["us_per_launch"], 3)}
+    if d1 is None:
+        print(json.dumps({"metric": METRIC, "matvec": mv, "roofline": roof}), flush=True)
+        return
     out = {
         "metric": METRIC,
         "value": round(d1["tok_s"], 2),

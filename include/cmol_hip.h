@@ -101,6 +101,11 @@ int cmolhip_act_prepare(cmolhip_ctx_t *c, const float *dx, int n, int cols, int 
                         const float *norm_w, void *op, float *ss);
 int cmolhip_gemm_prepared(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op, int n,
                           const float *ss, float eps, float *dy);
+/* cmolhip_gemm_prepared whose kernel records two hipEvent_t (start, stop)
+ * at its own start and end, for kernel-only timing. */
+int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op,
+                                int n, const float *ss, float eps, float *dy, void *ev_start,
+                                void *ev_stop);
 
 /* Reference kernel seam replacement (cmol_matmul_fn_t semantics on host
  * memory): out[m][n] = A[m][k] . B[k][n], A raw GGUF rows.  Uses the
@@ -112,11 +117,13 @@ int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a,
 /* Decode attention (reference src/attn.c:103-137) for `n` sessions whose
  * fp32 or fp16 caches are stacked as [n][n_kv][max_ctx][d_head]; q is
  * [n][n_heads*d_head] after RoPE, seqlen[n] (device int32) the number of
- * positions attended, out [n][n_heads*d_head].  Device pointers. */
+ * positions attended, out [n][n_heads*d_head].  Each work-group covers
+ * `split` positions (a multiple of 64; 0 picks 64) and splits are merged
+ * with log-sum-exp rescaling.  Device pointers. */
 int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q,
                         const void *kcache, const void *vcache,
                         const int32_t *seqlen, int n_heads, int n_kv,
-                        int d_head, int max_ctx, int kv_f16, float *out);
+                        int d_head, int max_ctx, int kv_f16, int split, float *out);
 
 /* ---- whole-model decode path ------------------------------------------- */
 typedef struct cmolhip_model cmolhip_model_t;

@@ -300,7 +300,14 @@ int cmolhip_act_prepare(cmolhip_ctx_t *c, const float *dx, int n, int cols, int 
 int cmolhip_gemm_prepared(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op, int n,
                           const float *ss, float eps, float *dy)
 {
-    if (!c || !w || !op || !dy || n < 1 || n > 32) return E_ARGS;
+    return cmolhip_gemm_prepared_timed(c, w, op, n, ss, eps, dy, nullptr, nullptr);
+}
+
+int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op,
+                                int n, const float *ss, float eps, float *dy, void *ev_start,
+                                void *ev_stop)
+{
+    if (!c || !w || !op || !dy || n < 1 || n > 32 || (!ev_start != !ev_stop)) return E_ARGS;
     GemvArgs a{};
     a.w = to_qt(*w);
     a.in.q = (const _Float16 *)op;
@@ -312,6 +319,8 @@ int cmolhip_gemm_prepared(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const vo
     a.out = dy;
     a.out_stride = w->rows;
     a.n = n;
+    a.ev_start = (hipEvent_t)ev_start;
+    a.ev_stop = (hipEvent_t)ev_stop;
     return launch_gemv(a, EPI_STORE, c->stream);
 }
 
@@ -368,12 +377,13 @@ int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float
 
 int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kcache,
                         const void *vcache, const int32_t *seqlen, int n_heads, int n_kv, int d_head,
-                        int max_ctx, int kv_f16, float *out)
+                        int max_ctx, int kv_f16, int split, float *out)
 {
     if (!c || n < 1 || !q || !kcache || !vcache || !seqlen || !out || n_kv < 1 || n_heads < n_kv ||
-        n_heads % n_kv || max_ctx < 1)
+        n_heads % n_kv || max_ctx < 1 || split < 0 || split % 64)
         return E_ARGS;
-    const int G = n_heads / n_kv, split = 64, ms = attn_max_splits(max_ctx, split);
+    if (!split) split = 64;
+    const int G = n_heads / n_kv, ms = attn_max_splits(max_ctx, split);
     const size_t mark = arena_mark(c);
     int rc = E_OK;
     do {
@@ -450,7 +460,7 @@ struct Batch {
     std::mutex mu;
 };
 
-constexpr int ATTN_SPLIT_MIN = 64, ATTN_SPLIT_MAX = 256;
+constexpr int ATTN_SPLIT_MIN = 64, ATTN_SPLIT_MAX = 1024;
 
 int pick_split(int max_ctx)
 {

@@ -5,6 +5,8 @@
 #include "common.h"
 #include "kernels.h"
 
+#include <hip/hip_ext.h>
+
 #include <cstdlib>
 
 // Launch shape of one matvec (host-computed, see plan_gemv).
@@ -426,12 +428,16 @@ static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
     // ring depth: the short ring when a wave's whole run fits it
     constexpr int UL = (DT == DT_Q8_0) ? 6 : 8, US = UL / 2;
     const int len = chunked ? ((a.w.block_quads + sh.qpc * NW - 1) / (sh.qpc * NW)) * sh.qpc : sh.qpc;
+    auto go = [&](auto kern) {
+        if (a.ev_start) hipExtLaunchKernelGGL(kern, grid, block, lds, s, a.ev_start, a.ev_stop, 0, a, sh);
+        else hipLaunchKernelGGL(kern, grid, block, lds, s, a, sh);
+    };
     if (chunked) {
-        if (len <= US) hipLaunchKernelGGL((k_gemv<DT, NW, NG, true, US>), grid, block, lds, s, a, sh);
-        else hipLaunchKernelGGL((k_gemv<DT, NW, NG, true, UL>), grid, block, lds, s, a, sh);
+        if (len <= US) go(k_gemv<DT, NW, NG, true, US>);
+        else go(k_gemv<DT, NW, NG, true, UL>);
     } else {
-        if (len <= US) hipLaunchKernelGGL((k_gemv<DT, NW, NG, false, US>), grid, block, lds, s, a, sh);
-        else hipLaunchKernelGGL((k_gemv<DT, NW, NG, false, UL>), grid, block, lds, s, a, sh);
+        if (len <= US) go(k_gemv<DT, NW, NG, false, US>);
+        else go(k_gemv<DT, NW, NG, false, UL>);
     }
     return 0;
 }

@@ -106,6 +106,8 @@ struct GemvArgs {
     int pos_stride;
     // EPI_LOGITS
     unsigned long long *argmax;   // ARGMAX_SLOTS slots per vector
+    // when set, recorded at the kernel's own start and end (kernel timing)
+    hipEvent_t ev_start, ev_stop;
 };
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);

@@ -88,9 +88,11 @@ SIGNATURES = [
     ("cmolhip_act_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("cmolhip_act_prepare", C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P, P]),
     ("cmolhip_gemm_prepared", C.c_int, [P, C.POINTER(QTensor), P, C.c_int, P, C.c_float, P]),
+    ("cmolhip_gemm_prepared_timed", C.c_int, [P, C.POINTER(QTensor), P, C.c_int, P, C.c_float, P,
+                                              P, P]),
     ("cmolhip_matmul_host", C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int]),
     ("cmolhip_attn_decode", C.c_int, [P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int,
-                                      C.c_int, C.c_int, P]),
+                                      C.c_int, C.c_int, C.c_int, P]),
     ("cmolhip_model_plan", C.c_int, [P, C.POINTER(C.c_size_t)]),
     ("cmolhip_model_create", C.c_int, [P, C.c_int, C.POINTER(P)]),
     ("cmolhip_model_destroy", None, [P]),

@@ -133,27 +133,38 @@ def test_gemv_reference_kats(ctx):
     assert ctx.gemm(t2, x2)[0].tolist() == [11.0]
 
 
-@pytest.mark.parametrize("n_heads,n_kv,d_head,lens", [
-    (9, 3, 64, [1, 17, 160]), (16, 4, 128, [2304, 5, 700]), (15, 5, 64, [64, 1024]),
-    (4, 4, 128, [333])])
-def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens):
+@pytest.mark.parametrize("n_heads,n_kv,d_head,lens,split,kv_f16", [
+    (9, 3, 64, [1, 17, 160], 64, 0), (16, 4, 128, [2304, 5, 700], 64, 0),
+    (15, 5, 64, [64, 1024], 64, 0), (4, 4, 128, [333], 64, 0),
+    (16, 4, 128, [2304, 5, 700, 1], 256, 0), (16, 4, 128, [3000, 64, 65, 129], 192, 1),
+    (9, 3, 64, [1, 17, 160, 999], 1024, 1), (4, 2, 16, [70, 3], 128, 0),
+    (8, 1, 32, [300], 64, 1), (8, 8, 256, [200, 77], 128, 0)])
+def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16):
+    """Ragged lengths across splits of one or several 64-position chunks,
+    fp32 and fp16 caches (the oracle reads the same rounded fp16 values)."""
     n = len(lens)
     max_ctx = max(lens)
-    rng = np.random.default_rng(n_heads * 100 + d_head)
+    rng = np.random.default_rng(n_heads * 100 + d_head + split)
     q = rng.standard_normal((n, n_heads * d_head)).astype(np.float32)
     kc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
     vc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
+    if kv_f16:
+        kc16, vc16 = kc.astype(np.float16), vc.astype(np.float16)
+        kc, vc = kc16.astype(np.float32), vc16.astype(np.float32)
+        dk, dv = ctx.upload(kc16), ctx.upload(vc16)
+    else:
+        dk, dv = ctx.upload(kc), ctx.upload(vc)
     sl = np.array(lens, np.int32)
-    dq, dk, dv, ds = ctx.upload(q), ctx.upload(kc), ctx.upload(vc), ctx.upload(sl)
+    dq, ds = ctx.upload(q), ctx.upload(sl)
     dout = ctx.alloc(q.nbytes)
     import ctypes as C
     gpu.check(gpu.lib().cmolhip_attn_decode(ctx.h, n, C.c_void_p(dq), C.c_void_p(dk), C.c_void_p(dv),
-                                            C.c_void_p(ds), n_heads, n_kv, d_head, max_ctx, 0,
-                                            C.c_void_p(dout)), "attn")
+                                            C.c_void_p(ds), n_heads, n_kv, d_head, max_ctx, kv_f16,
+                                            split, C.c_void_p(dout)), "attn")
     got = ctx.d2h(dout, q.shape, np.float32)
     for i, L in enumerate(lens):
         # oracle cache layout: [pos][n_kv][d_head]
         kref = np.ascontiguousarray(kc[i].transpose(1, 0, 2)[:L])
         vref = np.ascontiguousarray(vc[i].transpose(1, 0, 2)[:L])
         want = O.attention(q[i], kref, vref, L, n_heads, n_kv, d_head)
-        assert_close(got[i], want, f"attention session {i} len {L}")
+        assert_close(got[i], want, f"attention session {i} len {L} split {split}")
