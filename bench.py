@@ -90,15 +90,23 @@ def bench_matvec(rows, cols, n, copies, launches):
             "frac_of_peak": b / per_launch_s / 1e9 / HBM_PEAK_GBPS}
 
 
-def bench_decode_1(path, spec, prompt_len, steps, warmup):
-    max_ctx = prompt_len + warmup + steps + 8
+def bench_decode_1(path, spec, prompt_len, steps, warmup, synthetic_ctx=0):
+    """Single-session greedy decode after a prompt_len-token prefill, or (with
+    synthetic_ctx > 0) after filling the KV cache with that many synthetic
+    positions instead of running a prefill."""
+    ctx_len = synthetic_ctx or prompt_len
+    max_ctx = ctx_len + warmup + steps + 8
     m = native.Model(path, max_ctx=max_ctx, max_sessions=1)
     s = m.acquire()
-    prompt = synth.tokens(prompt_len, 42, spec.vocab)
     t0 = time.perf_counter()
-    tok, _ = s.prefill(prompt)
+    if synthetic_ctx:
+        s.fill_kv(synthetic_ctx, seed=3)
+        tok = 1
+    else:
+        prompt = synth.tokens(prompt_len, 42, spec.vocab)
+        tok, _ = s.prefill(prompt)
     prefill_s = time.perf_counter() - t0
-    pos = prompt_len
+    pos = ctx_len
     for _ in range(warmup):
         tok, _ = s.forward(tok, pos)
         pos += 1
@@ -116,9 +124,11 @@ def bench_decode_1(path, spec, prompt_len, steps, warmup):
     dev_ms = ev.elapsed()
     ev.close()
     m.close()
-    return {"tok_s": steps / wall, "ms_per_step": wall * 1e3 / steps,
-            "device_ms_per_step": dev_ms / steps, "prefill_tok_s": prompt_len / prefill_s,
-            "prefill_s": prefill_s}
+    out = {"tok_s": steps / wall, "ms_per_step": wall * 1e3 / steps,
+           "device_ms_per_step": dev_ms / steps, "context": ctx_len}
+    if not synthetic_ctx:
+        out.update(prefill_tok_s=prompt_len / prefill_s, prefill_s=prefill_s)
+    return out
 
 
 def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
@@ -146,6 +156,20 @@ def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
     return {"tok_s": sessions * steps / wall, "ms_per_step": wall * 1e3 / steps,
             "sessions": sessions, "mean_ctx": float(np.mean(lens)),
             "kv_bytes_per_step": kv_bytes}
+
+
+def recorded_traffic(name):
+    """HBM bytes per launch of the roofline kernel from its counter summary
+    under profiles/ (two rocprofv3 counter passes, FETCH_SIZE and WRITE_SIZE,
+    scaled by a copy of known size); None when the summary is absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def copy_calibration(mb, reps=4):
@@ -190,6 +214,9 @@ def main():
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--skip", default="", help="comma list of: decode,multi,matvec,cpu")
+    ap.add_argument("--synthetic-context", type=int, default=0,
+                    help="decode after filling the KV cache with this many synthetic positions "
+                         "instead of a prefill (profiling runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run device-to-device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -209,7 +236,7 @@ def main():
     d1 = None
     if "decode" not in skip:
         log("single-session decode")
-        d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup)
+        d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup, args.synthetic_context)
         log(json.dumps(d1))
     if args.copy_mb:
         log(json.dumps(copy_calibration(args.copy_mb)))
@@ -236,7 +263,8 @@ def main():
     if mv:
         r = mv[0]
         roof = {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(r["frac_of_peak"], 4), "traffic": None,
+                "unit": "GB/s", "frac": round(r["frac_of_peak"], 4),
+                "traffic": recorded_traffic("gemv_q4_11008x2048_traffic.txt"),
                 "kernel": "k_gemv<Q4_0> 11008x2048 n=1",
                 "bytes_per_launch": r["bytes_per_launch"],
                 "us_per_launch": round(r["us_per_launch"], 3)}
@@ -257,8 +285,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded random weights ~N(0,0.02), seeded random prompt ids)",
         "config": {"workload": "SmolLM3-3B-shaped Q4_0 (Q8_0 tied embd/LM head), 1 session, "
-                               f"greedy decode after a {args.prompt}-token prompt",
-                   "sessions": 1, "prompt": args.prompt,
+                               + (f"greedy decode at a {args.synthetic_context}-position synthetic "
+                                  "KV context" if args.synthetic_context else
+                                  f"greedy decode after a {args.prompt}-token prompt"),
+                   "sessions": 1, "prompt": 0 if args.synthetic_context else args.prompt,
                    "weight_bytes_per_token": weight_bytes,
                    "effective_weight_GBps": round(weight_bytes * d1["tok_s"] / 1e9, 1)},
         "decode_1": d1,
