@@ -120,3 +120,56 @@ def test_smollm2_135m_greedy_128(gpu, model_dir):
         ref = om2.forward(int(t), p)
     assert close_frac(lg, ref) == 1.0
     m.close()
+
+
+@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "micro-q8_0"])
+def test_decode_batch_matches_oracle(gpu, model_dir, preset):
+    """Lock-step decode of several sessions with ragged prompt lengths (one
+    launch per stage for all of them) continues every session exactly as the
+    oracle decodes it alone."""
+    spec = synth.PRESETS[preset].replace(wstd=0.08)
+    path = synth.model_file(spec, model_dir)
+    lens = [3, 17, 1, 40, 8, 25]
+    prompts = [synth.tokens(L, 100 + i, spec.vocab) for i, L in enumerate(lens)]
+    steps = 12
+    m = native.Model(path, max_ctx=96, max_sessions=len(lens))
+    ss = [m.acquire() for _ in lens]
+    toks = np.array([s.prefill(p)[0] for s, p in zip(ss, prompts)], np.int32)
+    got = [toks.copy()]
+    for _ in range(steps):
+        toks = native.decode_batch(ss, toks)
+        got.append(toks.copy())
+    got = np.stack(got, 1)
+    m.close()
+    for i, p in enumerate(prompts):
+        om = O.Model(path, 96)
+        want = om.generate(p, steps + 1)
+        assert got[i].tolist() == want.tolist(), f"session {i} (prompt {lens[i]})"
+
+
+@pytest.mark.parametrize("preset,sessions,lo,hi", [("smollm2-360m-q5_0", 16, 64, 1024),
+                                                   ("small-q4_0", 32, 512, 16384)])
+def test_decode_batch_matches_single_session_steps(gpu, model_dir, preset, sessions, lo, hi):
+    """Config-shaped lock-step batches over ragged synthetic KV caches give the
+    same next tokens as stepping each session alone (the single-vector path
+    is checked against the oracle above); a differing token is only allowed
+    where the two best logits are within the matvec tolerance."""
+    lens = synth.uniform_lengths(sessions, lo, hi, seed=5) if hi <= 1024 else \
+        synth.log_uniform_lengths(sessions, lo, hi, seed=7)
+    max_ctx = int(max(lens)) + 8
+    spec = synth.PRESETS[preset]
+    spec = spec.replace(ctx_len=max(spec.ctx_len, max_ctx))
+    path = synth.model_file(spec, model_dir)
+    toks = synth.tokens(sessions, 9, spec.vocab)
+    mb = native.Model(path, max_ctx=max_ctx, max_sessions=sessions)
+    bs = [mb.acquire() for _ in range(sessions)]
+    for i, s in enumerate(bs):
+        s.fill_kv(int(lens[i]), seed=1000 + i)
+    got = native.decode_batch(bs, toks)
+    for i, s in enumerate(bs):   # same state again, one session at a time
+        s.fill_kv(int(lens[i]), seed=1000 + i)
+        am, lg = s.forward(int(toks[i]), int(lens[i]), spec.vocab)
+        if am != got[i]:
+            top = np.sort(lg)[-2:]
+            assert top[1] - top[0] <= 1e-4 + 1e-3 * abs(top[1]), f"session {i}: {got[i]} vs {am}"
+    mb.close()
