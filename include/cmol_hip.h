@@ -131,6 +131,7 @@ typedef struct cmolhip_model cmolhip_model_t;
 typedef struct {
     int32_t n_layers, n_heads, n_kv_heads, d_model, d_head, d_ffn, vocab;
     int32_t max_ctx, max_sessions, no_rope_interval, kv_f16;
+    int32_t prefill_chunk;   /* prompt tokens per batched prefill pass (<= 0: 512) */
     float   rope_base, rms_eps;
 } cmolhip_hparams_t;
 
@@ -170,8 +171,9 @@ int cmolhip_decode(cmolhip_model_t *m, int slot, int32_t token, int32_t pos,
 int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots,
                          const int32_t *tokens, const int32_t *pos,
                          float *logits_host, int32_t *argmax);
-/* Prompt of n tokens at positions pos0.. into session `slot`; outputs as in
- * cmolhip_decode for the last prompt token. */
+/* Prompt of n tokens at positions pos0.. into session `slot`, in batched
+ * passes of prefill_chunk tokens (prompt GEMMs on MFMA, causal attention
+ * over the cache); outputs as in cmolhip_decode for the last prompt token. */
 int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n,
                     int32_t pos0, float *logits_host, int32_t *argmax);
 

@@ -451,8 +451,7 @@ struct Batch {
     float *ss_a = nullptr, *ss_b = nullptr;   // sum-of-squares partials [cap][d]
     unsigned long long *argmax = nullptr;     // [cap][ARGMAX_SLOTS]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
-    int32_t *prompt_steps = nullptr;          // device [max_ctx][3] (cap == 1 batches)
-    int32_t *h_steps = nullptr;               // pinned [max(cap, max_ctx)][3]
+    int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
     unsigned long long *h_argmax = nullptr;   // pinned [cap][ARGMAX_SLOTS]
     hipGraph_t graph = nullptr;
@@ -460,7 +459,38 @@ struct Batch {
     std::mutex mu;
 };
 
+// Buffers of a batched prompt pass of up to `cap` tokens of one session
+// (shared by the sessions; prefills are serialised by `mu`).
+struct Prefill {
+    int cap = 0;
+    int split = 1024, max_splits = 1;         // attention splits of the pass
+    int32_t *steps = nullptr;                 // device [cap][3] {token, pos, seqlen}
+    int32_t *slot_ids = nullptr;              // device [cap]
+    float *x = nullptr, *q = nullptr;
+    _Float16 *op_qkv = nullptr, *op_o = nullptr, *op_gu = nullptr, *op_dn = nullptr,
+             *op_lm = nullptr;
+    float *ss_a = nullptr, *ss_b = nullptr;   // [cap][d]
+    float *pm = nullptr, *pl = nullptr, *po = nullptr;
+    int32_t *h_steps = nullptr;               // pinned [cap][3]
+    int32_t *h_slots = nullptr;               // pinned [cap]
+    std::mutex mu;
+};
+
 constexpr int ATTN_SPLIT_MIN = 64, ATTN_SPLIT_MAX = 1024;
+
+int prefill_cap(const cmolhip_hparams_t &h)
+{
+    const int c = h.prefill_chunk > 0 ? h.prefill_chunk : 512;
+    return c < h.max_ctx ? c : h.max_ctx;
+}
+
+// Positions per attention work-group in a prompt pass: at most 16 splits.
+int prefill_split(int max_ctx)
+{
+    int s = (max_ctx + 15) / 16;
+    s = (s + 63) / 64 * 64;
+    return s < 1024 ? 1024 : s;
+}
 
 int pick_split(int max_ctx)
 {
@@ -564,7 +594,7 @@ int validate_desc(const cmolhip_model_desc_t *d)
 }
 
 // Buffers of one batch, in allocation order (mirrored by build_batch).
-void plan_batch(Plan &P, const cmolhip_hparams_t &h, int cap, int ms, int prompt)
+void plan_batch(Plan &P, const cmolhip_hparams_t &h, int cap, int ms)
 {
     const size_t np = (size_t)h.n_kv_heads * ms * (h.n_heads / h.n_kv_heads);
     P.add((size_t)cap * 3 * 4);
@@ -583,7 +613,28 @@ void plan_batch(Plan &P, const cmolhip_hparams_t &h, int cap, int ms, int prompt
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * h.d_head * 4);
-    if (prompt) P.add((size_t)h.max_ctx * 3 * 4);
+}
+
+// Buffers of the prompt pass, in allocation order (mirrored by build_prefill).
+void plan_prefill(Plan &P, const cmolhip_hparams_t &h)
+{
+    const int cap = prefill_cap(h);
+    const int ms = attn_max_splits(h.max_ctx, prefill_split(h.max_ctx));
+    const size_t np = (size_t)h.n_kv_heads * ms * (h.n_heads / h.n_kv_heads);
+    P.add((size_t)cap * 3 * 4);
+    P.add((size_t)cap * 4);
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * h.d_model * 4);
+    P.add(act_bytes(h.d_model, cap));
+    P.add(act_bytes(h.d_model, cap));
+    P.add(act_bytes(h.d_model, cap));
+    P.add(act_bytes(h.d_ffn, cap));
+    P.add(act_bytes(h.d_model, cap));
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * h.d_model * 4);
+    P.add((size_t)cap * np * 4);
+    P.add((size_t)cap * np * 4);
+    P.add((size_t)cap * np * h.d_head * 4);
 }
 
 Plan make_plan(const cmolhip_model_desc_t *d)
@@ -624,8 +675,9 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(kv_elems * esz);
     P.add(kv_elems * esz);
     P.add((size_t)h.n_kv_heads * h.max_ctx * h.d_head * 4);         // scratch
-    for (int s = 0; s < h.max_sessions; s++) plan_batch(P, h, 1, ms, 1);
-    plan_batch(P, h, h.max_sessions, ms, 0);                        // lock-step batch
+    for (int s = 0; s < h.max_sessions; s++) plan_batch(P, h, 1, ms);
+    plan_batch(P, h, h.max_sessions, ms);                           // lock-step batch
+    plan_prefill(P, h);
     return P;
 }
 
@@ -642,6 +694,7 @@ struct cmolhip_model {
     int split = 64, max_splits = 1;
     std::vector<std::unique_ptr<Batch>> slots;   // one single-vector batch per session
     std::unique_ptr<Batch> multi;                // lock-step batch over sessions
+    std::unique_ptr<Prefill> pf;                 // prompt passes
     std::mutex scratch_mu;
     bool use_graph = true;
 };
@@ -781,6 +834,113 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
     return E_OK;
 }
 
+// One batched prompt pass of n tokens of one session (steps and slot ids
+// already on the device): embedding, L x (QKV GEMM + RoPE + KV write, causal
+// attention over the cache, Wo GEMM + residual, gate/up GEMM + SwiGLU, down
+// GEMM + residual); with `last`, the final token's LM-head operand is
+// extracted into the session's decode batch B and its logits computed there.
+int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hipStream_t st)
+{
+    const cmolhip_hparams_t &hp = m->hp;
+    const int d = hp.d_model, kvd = hp.n_kv_heads * hp.d_head, P = d;
+    const float eps = hp.rms_eps;
+    KVRef kv;
+    kv.k_base = m->kbase;
+    kv.v_base = m->vbase;
+    kv.slot_stride = m->slot_stride;
+    kv.slot_ids = F.slot_ids;
+    RC(launch_embed(to_qt(m->embd), F.steps, 3, F.x, d,
+                    act_out(F.op_qkv, m->layers[0].qkv.dtype, n, m->layers[0].attn_norm, F.ss_a, P),
+                    nullptr, n, st));
+    int ss_count = d / 32;
+    const int tile_count = (d + 15) / 16;   // GEMM residual partials: one per 16 rows
+    for (int l = 0; l < hp.n_layers; l++) {
+        const MLayer &L = m->layers[l];
+        kv.layer_off = (size_t)l * m->layer_stride;
+        GemvArgs g{};
+        g.w = to_qt(L.qkv);
+        g.in = act_in(F.op_qkv, n, F.ss_a, ss_count, P, eps);
+        g.out = F.q;
+        g.out_stride = d;
+        g.n = n;
+        g.nq = d;
+        g.nkv = kvd;
+        g.d_head = hp.d_head;
+        g.max_ctx = hp.max_ctx;
+        g.kv_f16 = hp.kv_f16;
+        g.rope_on = L.rope_on;
+        g.rope = m->rope;
+        g.kv = kv;
+        g.pos = F.steps + 1;
+        g.pos_stride = 3;
+        RC(launch_gemm(g, EPI_QKV, st));
+
+        AttnArgs at{};
+        at.q = F.q;
+        at.q_stride = d;
+        at.kv = kv;
+        at.seqlen = F.steps + 2;
+        at.seqlen_stride = 3;
+        at.n = n;
+        at.n_heads = hp.n_heads;
+        at.n_kv = hp.n_kv_heads;
+        at.d_head = hp.d_head;
+        at.max_ctx = hp.max_ctx;
+        at.kv_f16 = hp.kv_f16;
+        at.split = F.split;
+        at.max_splits = F.max_splits;
+        at.pm = F.pm;
+        at.pl = F.pl;
+        at.po = F.po;
+        at.out = nullptr;
+        at.next = act_out(F.op_o, L.o.dtype, n, nullptr, nullptr, 0);
+        RC(launch_attn(at, st));
+
+        GemvArgs go{};
+        go.w = to_qt(L.o);
+        go.in = act_in(F.op_o, n, nullptr, 0, 0, eps);
+        go.out = F.x;
+        go.out_stride = d;
+        go.n = n;
+        go.next = act_out(F.op_gu, L.gu.dtype, n, L.ffn_norm, F.ss_b, P);
+        RC(launch_gemm(go, EPI_RESID, st));
+
+        GemvArgs gu{};
+        gu.w = to_qt(L.gu);
+        gu.in = act_in(F.op_gu, n, F.ss_b, tile_count, P, eps);
+        gu.out = nullptr;
+        gu.n = n;
+        gu.next = act_out(F.op_dn, L.down.dtype, n, nullptr, nullptr, 0);
+        RC(launch_gemm(gu, EPI_SWIGLU, st));
+
+        GemvArgs gd{};
+        gd.w = to_qt(L.down);
+        gd.in = act_in(F.op_dn, n, nullptr, 0, 0, eps);
+        gd.out = F.x;
+        gd.out_stride = d;
+        gd.n = n;
+        if (l + 1 < hp.n_layers)
+            gd.next = act_out(F.op_qkv, m->layers[l + 1].qkv.dtype, n, m->layers[l + 1].attn_norm, F.ss_a, P);
+        else
+            gd.next = act_out(F.op_lm, lm_tensor(m).dtype, n, m->out_norm, F.ss_a, P);
+        RC(launch_gemm(gd, EPI_RESID, st));
+        ss_count = tile_count;
+    }
+    if (!last) return E_OK;
+    // LM head for the last token only, through the session's decode buffers
+    RC(launch_act_extract(F.op_lm, d, n, n - 1, B.op_lm, F.ss_a, P, ss_count, B.ss_a, st));
+    HC(hipMemsetAsync(B.argmax, 0, ARGMAX_SLOTS * sizeof(unsigned long long), st));
+    GemvArgs gl{};
+    gl.w = to_qt(lm_tensor(m));
+    gl.in = act_in(B.op_lm, 1, B.ss_a, ss_count, ss_count, eps);
+    gl.out = B.logits;
+    gl.out_stride = hp.vocab;
+    gl.n = 1;
+    gl.argmax = B.argmax;
+    RC(launch_gemv(gl, EPI_LOGITS, st));
+    return E_OK;
+}
+
 int upload_norm(cmolhip_ctx_t *c, const cmolhip_host_tensor_t &t, float **dst)
 {
     RC(arena_get(c, (size_t)t.cols, dst));
@@ -799,7 +959,7 @@ int upload_q(cmolhip_ctx_t *c, int n, const cmolhip_host_tensor_t *const *ts, in
     return cmolhip_qtensor_upload(c, ts[0]->dtype, ts[0]->cols, fold, n, parts, rows, mode, stg, stg_bytes, out);
 }
 
-int build_batch(cmolhip_model *m, Batch &B, int cap, int prompt)
+int build_batch(cmolhip_model *m, Batch &B, int cap)
 {
     cmolhip_ctx_t *c = m->ctx;
     const cmolhip_hparams_t &h = m->hp;
@@ -822,13 +982,37 @@ int build_batch(cmolhip_model *m, Batch &B, int cap, int prompt)
     RC(arena_get(c, (size_t)cap * np, &B.pm));
     RC(arena_get(c, (size_t)cap * np, &B.pl));
     RC(arena_get(c, (size_t)cap * np * h.d_head, &B.po));
-    if (prompt) RC(arena_get(c, (size_t)h.max_ctx * 3, &B.prompt_steps));
     HC(hipMemsetAsync(B.steps, 0, (size_t)cap * 12, c->stream));
     HC(hipStreamCreateWithFlags(&B.st, hipStreamNonBlocking));
-    const size_t hs = (size_t)(prompt ? (h.max_ctx > cap ? h.max_ctx : cap) : cap) * 3 * 4;
-    HC(hipHostMalloc((void **)&B.h_steps, hs, hipHostMallocDefault));
+    HC(hipHostMalloc((void **)&B.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
     HC(hipHostMalloc((void **)&B.h_slots, (size_t)cap * 4, hipHostMallocDefault));
     HC(hipHostMalloc((void **)&B.h_argmax, (size_t)cap * ARGMAX_SLOTS * 8, hipHostMallocDefault));
+    return E_OK;
+}
+
+int build_prefill(cmolhip_model *m, Prefill &F)
+{
+    cmolhip_ctx_t *c = m->ctx;
+    const cmolhip_hparams_t &h = m->hp;
+    F.cap = prefill_cap(h);
+    F.split = prefill_split(h.max_ctx);
+    F.max_splits = attn_max_splits(h.max_ctx, F.split);
+    const int cap = F.cap;
+    const size_t np = (size_t)h.n_kv_heads * F.max_splits * (h.n_heads / h.n_kv_heads);
+    RC(arena_get(c, (size_t)cap * 3, &F.steps));
+    RC(arena_get(c, (size_t)cap, &F.slot_ids));
+    RC(arena_get(c, (size_t)cap * h.d_model, &F.x));
+    RC(arena_get(c, (size_t)cap * h.d_model, &F.q));
+    _Float16 **ops[5] = {&F.op_qkv, &F.op_o, &F.op_gu, &F.op_dn, &F.op_lm};
+    const int opk[5] = {h.d_model, h.d_model, h.d_model, h.d_ffn, h.d_model};
+    for (int i = 0; i < 5; i++) RC(cmolhip_alloc(c, act_bytes(opk[i], cap), ALIGN, (void **)ops[i]));
+    RC(arena_get(c, (size_t)cap * h.d_model, &F.ss_a));
+    RC(arena_get(c, (size_t)cap * h.d_model, &F.ss_b));
+    RC(arena_get(c, (size_t)cap * np, &F.pm));
+    RC(arena_get(c, (size_t)cap * np, &F.pl));
+    RC(arena_get(c, (size_t)cap * np * h.d_head, &F.po));
+    HC(hipHostMalloc((void **)&F.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
+    HC(hipHostMalloc((void **)&F.h_slots, (size_t)cap * 4, hipHostMallocDefault));
     return E_OK;
 }
 
@@ -883,12 +1067,14 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     for (int s = 0; s < h.max_sessions; s++) {
         m->slots.emplace_back(new Batch());
         Batch &B = *m->slots.back();
-        RC(build_batch(m, B, 1, 1));
+        RC(build_batch(m, B, 1));
         const int32_t sid = s;
         RC(cmolhip_memcpy_h2d(c, B.slot_ids, &sid, 4));
     }
     m->multi.reset(new Batch());
-    RC(build_batch(m, *m->multi, h.max_sessions, 0));
+    RC(build_batch(m, *m->multi, h.max_sessions));
+    m->pf.reset(new Prefill());
+    RC(build_prefill(m, *m->pf));
     HC(hipStreamSynchronize(c->stream));
     if (m->use_graph) {
         for (auto &sp : m->slots) {
@@ -982,6 +1168,10 @@ void cmolhip_model_destroy(cmolhip_model_t *m)
     if (m->ctx) (void)hipSetDevice(m->ctx->device);
     for (auto &sp : m->slots) destroy_batch(*sp);
     if (m->multi) destroy_batch(*m->multi);
+    if (m->pf) {
+        if (m->pf->h_steps) (void)hipHostFree(m->pf->h_steps);
+        if (m->pf->h_slots) (void)hipHostFree(m->pf->h_slots);
+    }
     cmolhip_ctx_destroy(m->ctx);
     delete m;
 }
@@ -1017,16 +1207,22 @@ int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, 
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->hp.vocab) return E_ARGS;
     Batch &B = *m->slots[slot];
+    Prefill &F = *m->pf;
     std::lock_guard<std::mutex> g(B.mu);
-    for (int i = 0; i < n; i++) {
-        B.h_steps[3 * i + 0] = tokens[i];
-        B.h_steps[3 * i + 1] = pos0 + i;
-        B.h_steps[3 * i + 2] = pos0 + i + 1;
-    }
-    HC(hipMemcpyAsync(B.prompt_steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
-    for (int i = 0; i < n; i++) {
-        HC(hipMemcpyAsync(B.steps, B.prompt_steps + 3 * i, 12, hipMemcpyDeviceToDevice, B.st));
-        RC(run_single(m, B));
+    std::lock_guard<std::mutex> gf(F.mu);
+    for (int i = 0; i < F.cap; i++) F.h_slots[i] = slot;
+    HC(hipMemcpyAsync(F.slot_ids, F.h_slots, (size_t)F.cap * 4, hipMemcpyHostToDevice, B.st));
+    for (int c0 = 0; c0 < n; c0 += F.cap) {
+        const int nc = n - c0 < F.cap ? n - c0 : F.cap;
+        // the pinned step records are reused: wait for the previous pass's copy
+        if (c0) HC(hipStreamSynchronize(B.st));
+        for (int i = 0; i < nc; i++) {
+            F.h_steps[3 * i + 0] = tokens[c0 + i];
+            F.h_steps[3 * i + 1] = pos0 + c0 + i;
+            F.h_steps[3 * i + 2] = pos0 + c0 + i + 1;
+        }
+        HC(hipMemcpyAsync(F.steps, F.h_steps, (size_t)nc * 12, hipMemcpyHostToDevice, B.st));
+        RC(enqueue_prefill(m, F, B, nc, c0 + nc == n, B.st));
     }
     return finish(m, B, 1, logits_host, argmax);
 }

@@ -27,6 +27,9 @@
 int launch_gemv_q4(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemv_q5(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemv_q8(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemm_q4(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemm_q5(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemm_q8(const GemvArgs &a, int epi, hipStream_t s);
 
 size_t act_bytes(int K, int n)
 {
@@ -43,6 +46,20 @@ int launch_gemv(const GemvArgs &a, int epi, hipStream_t s)
     case DT_Q4_0: rc = launch_gemv_q4(a, epi, s); break;
     case DT_Q5_0: rc = launch_gemv_q5(a, epi, s); break;
     case DT_Q8_0: rc = launch_gemv_q8(a, epi, s); break;
+    default: return -4;
+    }
+    if (rc) return rc;
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_gemm(const GemvArgs &a, int epi, hipStream_t s)
+{
+    if (a.n < 1 || a.in.nrows != 2 * a.n || !a.in.q) return -6;
+    int rc;
+    switch (a.w.dtype) {
+    case DT_Q4_0: rc = launch_gemm_q4(a, epi, s); break;
+    case DT_Q5_0: rc = launch_gemm_q5(a, epi, s); break;
+    case DT_Q8_0: rc = launch_gemm_q8(a, epi, s); break;
     default: return -4;
     }
     if (rc) return rc;

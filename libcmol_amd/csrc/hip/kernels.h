@@ -111,6 +111,9 @@ struct GemvArgs {
 };
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);
+// The same product for many vectors (prompt tokens): 64 x 64 output tiles,
+// epilogues EPI_STORE..EPI_QKV; any n >= 1.
+int launch_gemm(const GemvArgs &a, int epi, hipStream_t s);
 // x [n][x_stride] fp32 -> operand (and sum-of-squares partials per 32 inputs).
 int launch_act_prep(const float *x, int x_stride, int K, int n, const ActOut &o, hipStream_t s);
 // Operand bytes for K inputs (padded to whole block quads) and n vectors.
@@ -142,6 +145,10 @@ int launch_kv_convert(const void *src, float *dst, int n_kv, int max_ctx,
                       int d_head, int n, int kv_f16, int to_ref, hipStream_t s);
 int launch_kv_import(const float *src, void *dst, int n_kv, int max_ctx,
                      int d_head, int n, int kv_f16, hipStream_t s);
+// Vector v of an n-vector operand (K inputs) -> one-vector operand, and its
+// sum-of-squares partials (ss_src may be null).
+int launch_act_extract(const _Float16 *src, int K, int n, int v, _Float16 *dst, const float *ss_src,
+                       int ss_stride, int ss_count, float *ss_dst, hipStream_t s);
 
 // Writes value v of input k of vector n into an operand (see ActOut).
 __device__ inline void act_put(const ActOut &o, int n, int k, float v)

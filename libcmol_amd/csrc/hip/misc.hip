@@ -102,3 +102,29 @@ int launch_kv_import(const float *src, void *dst, int n_kv, int max_ctx, int d_h
                        d_head, n, kv_f16);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
+
+// Operand rows of vector v of an n-vector operand (K inputs) -> a one-vector
+// operand, plus that vector's sum-of-squares partials.
+__global__ void k_act_extract(const _Float16 *src, int K, int n, int v, _Float16 *dst,
+                              const float *ss_src, int ss_stride, int ss_count, float *ss_dst)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // (block, group) segment
+    const int segs = (K / 32) * 4;
+    if (i < segs) {
+        const uint4 *s = (const uint4 *)(src + ((size_t)i * 2 * n + 2 * v) * 8);
+        uint4 *d = (uint4 *)(dst + (size_t)i * 2 * 8);
+        d[0] = s[0];
+        d[1] = s[1];
+    }
+    if (ss_src && i < ss_count) ss_dst[i] = ss_src[(size_t)v * ss_stride + i];
+}
+
+int launch_act_extract(const _Float16 *src, int K, int n, int v, _Float16 *dst, const float *ss_src,
+                       int ss_stride, int ss_count, float *ss_dst, hipStream_t s)
+{
+    const int segs = (K / 32) * 4;
+    const int work = segs > ss_count ? segs : ss_count;
+    hipLaunchKernelGGL(k_act_extract, dim3((work + 255) / 256), dim3(256), 0, s, src, K, n, v, dst,
+                       ss_src, ss_stride, ss_count, ss_dst);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}

@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void k_embed(QTensor t, const int32_t *__restr
     if (s >= n) return;
     const int nb = t.cols / 32;
     int tok = token[s * token_stride];
-    if (blockIdx.x == 0)
+    if (argmax && blockIdx.x == 0)
         for (int i = threadIdx.x; i < ARGMAX_SLOTS; i += blockDim.x) argmax[(size_t)s * ARGMAX_SLOTS + i] = 0ull;
     if (tok < 0 || tok >= t.rows) tok = 0;
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;

@@ -121,6 +121,7 @@ static cmol_err_t make_desc(cmol_model_t *m, cmolhip_model_desc_t *d, cmol_arena
     d->hp.max_sessions = m->cfg.max_sessions;
     d->hp.no_rope_interval = hp->no_rope_layer_interval;
     d->hp.kv_f16 = m->kv_f16;
+    d->hp.prefill_chunk = m->cfg.prefill_chunk;
     d->hp.rope_base = hp->rope_freq_base;
     d->hp.rms_eps = hp->rms_norm_eps;
     cmol_tensor_t *embd = cmol_gguf_find_tensor(m->tensors, m->n_tensors, "token_embd.weight");

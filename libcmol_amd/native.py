@@ -247,10 +247,11 @@ class Ctx:
 # Model / sessions (public API + harness entry points)
 # ---------------------------------------------------------------------------
 class Model:
-    def __init__(self, path: str, max_ctx: int = 0, max_sessions: int = 1, log: bool = False):
+    def __init__(self, path: str, max_ctx: int = 0, max_sessions: int = 1, log: bool = False,
+                 prefill_chunk: int = 512):
         self._logs = []
         self._logfn = LOG_FN(lambda lvl, msg, ud: self._logs.append(msg.decode()))
-        cfg = Config(max_ctx, max_sessions, 512, self._logfn if log else LOG_FN(), None)
+        cfg = Config(max_ctx, max_sessions, prefill_chunk, self._logfn if log else LOG_FN(), None)
         err = C.c_int(0)
         self.h = lib().cmol_load(path.encode(), C.byref(cfg), C.byref(err))
         if not self.h:

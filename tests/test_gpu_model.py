@@ -173,3 +173,36 @@ def test_decode_batch_matches_single_session_steps(gpu, model_dir, preset, sessi
             top = np.sort(lg)[-2:]
             assert top[1] - top[0] <= 1e-4 + 1e-3 * abs(top[1]), f"session {i}: {got[i]} vs {am}"
     mb.close()
+
+
+@pytest.mark.parametrize("preset,chunk", [("small-q4_0", 16), ("small-q5_0", 7), ("small-q8_0-untied", 64),
+                                          ("micro-q4_0", 5)])
+def test_chunked_prefill_matches_oracle(gpu, model_dir, preset, chunk):
+    """A prompt longer than prefill_chunk runs as several batched passes (the
+    later ones attend to the cache the earlier ones wrote): logits after the
+    prompt, the whole KV cache and the greedy continuation match the oracle."""
+    spec = synth.PRESETS[preset].replace(wstd=0.08)
+    path = synth.model_file(spec, model_dir)
+    prompt = synth.tokens(45, 11, spec.vocab)
+    m = native.Model(path, max_ctx=64, max_sessions=1, prefill_chunk=chunk)
+    s = m.acquire()
+    am, lg = s.prefill(prompt, spec.vocab)
+    om = O.Model(path, 64)
+    for p, t in enumerate(prompt):
+        want = om.forward(int(t), p)
+    assert close_frac(lg, want) == 1.0
+    assert am == int(np.argmax(want))
+    ok, ov = om.kv()
+    kd = spec.n_kv_heads * spec.d_head
+    for layer in range(spec.n_layers):
+        k = np.zeros((45, kd), np.float32)
+        v = np.zeros((45, kd), np.float32)
+        native.check(native.lib().cmolhip_kv_download(m.device, s.slot, layer, 45,
+                                                       native.ptr(k), native.ptr(v)), "kv")
+        assert close_frac(k, ok[layer, :45].reshape(45, kd)) == 1.0
+        assert close_frac(v, ov[layer, :45].reshape(45, kd)) == 1.0
+    s.reset()
+    got = s.generate_ids(prompt, native.greedy_params(12), 12)
+    om2 = O.Model(path, 64)
+    assert got.tolist() == om2.generate(prompt, 12).tolist()
+    m.close()
