@@ -33,6 +33,7 @@ from libcmol_amd import hiprt, synth  # noqa: E402
 
 METRIC = "decode tok/s SmolLM3-3B Q4_0 (1 & 32 sessions); matvec HBM GB/s % of peak"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16 MFMA, MI355X
 
 
 def log(*a):
@@ -46,17 +47,20 @@ def q4_bytes(m, k, n):
     return m * (k // 32) * 18 + 4 * k * n + 4 * m * n
 
 
-def bench_matvec(rows, cols, n, copies, launches):
+def bench_matvec(rows, cols, n, copies, launches, fold=None):
     """Average duration of the Q4_0 matvec kernel over `copies` distinct
     weight buffers (defeating the 256 MB Infinity Cache): every launch records
     a pair of HIP events at the kernel's own start and end (on the stream it
     runs on).  The weights use the fold a model serving n sessions gives this
-    shape."""
-    fold = native.lib().cmolhip_pick_fold(rows, cols, n)
+    shape unless `fold` is given.  More than 32 vectors run the tiled MFMA
+    GEMM of the prompt pass."""
+    if fold is None:
+        fold = native.lib().cmolhip_pick_fold(rows, cols, n)
     w = synth.normal(rows * cols, seed=1234, stream=rows * 7 + cols, std=0.02)
     raw = synth.quantize(synth.Q4_0, w).reshape(rows, -1)
     tensor_bytes = native.lib().cmolhip_qtensor_bytes(2, rows, cols, fold)
-    arena = copies * (tensor_bytes + 4096) + raw.nbytes + 64 * cols * 4 + 64 * rows * 4 + (64 << 20)
+    arena = (copies * (tensor_bytes + 4096) + raw.nbytes + n * cols * 4 + n * rows * 4
+             + native.lib().cmolhip_act_bytes(cols, n) + (64 << 20))
     ctx = native.Ctx(arena)
     stg = ctx.alloc(raw.nbytes)
     ts = [ctx.qtensor([raw], 2, cols, [rows], staging_bytes=raw.nbytes, staging=stg, fold=fold)
@@ -85,9 +89,17 @@ def bench_matvec(rows, cols, n, copies, launches):
         ev.close()
     ctx.close()
     b = q4_bytes(rows, cols, n)
-    return {"shape": f"{rows}x{cols}", "n": n, "fold": fold, "us_per_launch": per_launch_s * 1e6,
-            "bytes_per_launch": b, "GBps": b / per_launch_s / 1e9,
-            "frac_of_peak": b / per_launch_s / 1e9 / HBM_PEAK_GBPS}
+    flops = 2.0 * rows * cols * n
+    out = {"shape": f"{rows}x{cols}", "n": n, "fold": fold, "us_per_launch": per_launch_s * 1e6,
+           "bytes_per_launch": b, "GBps": b / per_launch_s / 1e9,
+           "frac_of_peak": b / per_launch_s / 1e9 / HBM_PEAK_GBPS}
+    if n > 32:
+        # the tiled GEMM issues two f16 products per weight and vector (the
+        # operand's high and low parts): useful and issued MFMA rates
+        out.update(useful_TFLOPs=flops / per_launch_s / 1e12,
+                   mfma_TFLOPs=2 * flops / per_launch_s / 1e12,
+                   mfma_frac_of_peak=2 * flops / per_launch_s / 1e12 / MFMA_F16_PEAK_TFLOPS)
+    return out
 
 
 def bench_decode_1(path, spec, prompt_len, steps, warmup, synthetic_ctx=0):
@@ -213,7 +225,7 @@ def main():
     ap.add_argument("--sessions", type=int, default=32)
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
-    ap.add_argument("--skip", default="", help="comma list of: decode,multi,matvec,cpu")
+    ap.add_argument("--skip", default="", help="comma list of: decode,multi,matvec,gemm,cpu")
     ap.add_argument("--synthetic-context", type=int, default=0,
                     help="decode after filling the KV cache with this many synthetic positions "
                          "instead of a prefill (profiling runs)")
@@ -247,6 +259,13 @@ def main():
                 r = bench_matvec(rows, cols, n, copies=64, launches=256)
                 log(json.dumps(r))
                 mv.append(r)
+    gm = []
+    if "gemm" not in skip:
+        # the prompt pass's GEMM at M = 2048 tokens on the FFN shapes
+        for rows, cols in ((11008, 2048), (2048, 11008)):
+            r = bench_matvec(rows, cols, 2048, copies=2, launches=16, fold=1)
+            log(json.dumps(r))
+            gm.append(r)
     d32 = None
     if "multi" not in skip:
         log("32-session decode")
@@ -269,7 +288,7 @@ def main():
                 "bytes_per_launch": r["bytes_per_launch"],
                 "us_per_launch": round(r["us_per_launch"], 3)}
     if d1 is None:
-        print(json.dumps({"metric": METRIC, "matvec": mv, "roofline": roof}), flush=True)
+        print(json.dumps({"metric": METRIC, "matvec": mv, "gemm": gm, "roofline": roof}), flush=True)
         return
     out = {
         "metric": METRIC,
@@ -294,6 +313,7 @@ def main():
         "decode_1": d1,
         "decode_32": d32,
         "matvec": mv,
+        "prefill_gemm": gm,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -86,7 +86,9 @@ int cmolhip_dequant(cmolhip_ctx_t *c, const cmolhip_qtensor_t *t, float *dout);
 
 /* dy[n][rows] = W . dx[n][cols] for n activation vectors (fp32 accumulate).
  * When norm_w != NULL each x is RMS-normalised first (weights norm_w[cols],
- * epsilon eps).  n in 1..32.  Device pointers; runs on the context stream. */
+ * epsilon eps).  n in 1..65535: up to 32 vectors run the streaming matvec,
+ * more the tiled MFMA GEMM (64 vectors x 128 rows per work-group).  Device
+ * pointers; runs on the context stream. */
 int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx,
                  float *dy, int n, const float *norm_w, float eps);
 

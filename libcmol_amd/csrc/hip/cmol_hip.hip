@@ -23,6 +23,8 @@ namespace {
 
 constexpr int E_OK = 0, E_OOM = -1, E_INVALID = -3, E_UNSUPPORTED = -4, E_ARGS = -6;
 constexpr size_t ALIGN = 256;
+// vectors per matvec/GEMM call (the operand preparation grid's y extent)
+constexpr int GEMM_MAX_N = 65535;
 
 int herr(hipError_t e)
 {
@@ -285,7 +287,7 @@ size_t cmolhip_act_bytes(int cols, int n) { return (cols > 0 && n > 0) ? act_byt
 int cmolhip_act_prepare(cmolhip_ctx_t *c, const float *dx, int n, int cols, int dtype,
                         const float *norm_w, void *op, float *ss)
 {
-    if (!c || !dx || !op || n < 1 || n > 32 || cols < 32 || cols % 32) return E_ARGS;
+    if (!c || !dx || !op || n < 1 || n > GEMM_MAX_N || cols < 32 || cols % 32) return E_ARGS;
     if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0) return E_UNSUPPORTED;
     ActOut o{};
     o.q = (_Float16 *)op;
@@ -307,7 +309,7 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
                                 int n, const float *ss, float eps, float *dy, void *ev_start,
                                 void *ev_stop)
 {
-    if (!c || !w || !op || !dy || n < 1 || n > 32 || (!ev_start != !ev_stop)) return E_ARGS;
+    if (!c || !w || !op || !dy || n < 1 || n > GEMM_MAX_N || (!ev_start != !ev_stop)) return E_ARGS;
     GemvArgs a{};
     a.w = to_qt(*w);
     a.in.q = (const _Float16 *)op;
@@ -321,13 +323,15 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
     a.n = n;
     a.ev_start = (hipEvent_t)ev_start;
     a.ev_stop = (hipEvent_t)ev_stop;
-    return launch_gemv(a, EPI_STORE, c->stream);
+    // up to 32 vectors stream the weights once through the matvec; more go
+    // to the tiled MFMA GEMM
+    return n <= 32 ? launch_gemv(a, EPI_STORE, c->stream) : launch_gemm(a, EPI_STORE, c->stream);
 }
 
 int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx, float *dy, int n,
                  const float *norm_w, float eps)
 {
-    if (!c || !w || !dx || !dy || n < 1 || n > 32) return E_ARGS;
+    if (!c || !w || !dx || !dy || n < 1 || n > GEMM_MAX_N) return E_ARGS;
     const size_t mark = arena_mark(c);
     int rc = E_OK;
     do {
@@ -345,7 +349,7 @@ int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx, 
 int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float *b, int m, int k,
                         int n, int dtype)
 {
-    if (!c || !out || !a || !b || m < 1 || k < 32 || k % 32 || n < 1 || n > 32) return E_ARGS;
+    if (!c || !out || !a || !b || m < 1 || k < 32 || k % 32 || n < 1 || n > GEMM_MAX_N) return E_ARGS;
     if (!qbytes_aligned(dtype, m, k, 1)) return E_UNSUPPORTED;
     const size_t mark = arena_mark(c);
     int rc = E_OK;

@@ -102,6 +102,35 @@ def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
     assert_close(got, want, f"gemm q{dtype} {rows}x{cols} fold {fold} n {n}")
 
 
+@pytest.mark.parametrize("dtype,rows,cols,fold,n", [
+    (2, 384, 2048, 1, 33), (2, 256, 2048, 1, 64), (2, 300, 2048, 1, 130), (8, 576, 576, 1, 200),
+    (6, 320, 960, 1, 97), (6, 2560, 960, 1, 64), (2, 2048, 11008, 4, 65), (2, 3072, 2048, 4, 128),
+    (8, 200, 576, 8, 70), (6, 960, 960, 2, 96), (2, 37, 4096, 1, 40), (2, 512, 2048, 1, 512)])
+def test_gemm_tiled_matches_oracle(ctx, dtype, rows, cols, fold, n):
+    """More than 32 vectors run the tiled MFMA GEMM (prompt prefill): partial
+    row and vector tiles, folded weights read in place, and padding blocks."""
+    raw = random_blocks(dtype, rows, cols, seed=rows * 5 + cols + n)
+    x = np.random.default_rng(n + 1).standard_normal((n, cols)).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
+    got = ctx.gemm(t, x)
+    want = O.matmul(raw, np.ascontiguousarray(x.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"tiled gemm q{dtype} {rows}x{cols} fold {fold} n {n}")
+
+
+def test_gemm_tiled_rmsnorm_prologue(ctx):
+    """The GEMM applies the RMSNorm scale from the operand's sums of squares."""
+    rows, cols, n = 256, 960, 80
+    raw = random_blocks(6, rows, cols, seed=9)
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((n, cols)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    t = ctx.qtensor([raw], 6, cols, [rows])
+    got = ctx.gemm(t, x, norm_w=w, eps=1e-6)
+    xn = np.stack([O.rms_norm(xi, w, 1e-6) for xi in x])
+    want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, 6, O.AVX512).T
+    assert_close(got, want, "tiled gemm with rmsnorm")
+
+
 def test_gemv_rmsnorm_prologue(ctx):
     rows, cols, dtype = 256, 2048, 2
     raw = random_blocks(dtype, rows, cols, seed=9)
