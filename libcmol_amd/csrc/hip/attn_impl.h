@@ -1,0 +1,267 @@
+// attn_impl.h — split-K grouped-query decode attention over ragged KV
+// lengths, as work-group device functions shared by the attention kernels
+// (attn.hip) and the persistent decode kernel (persist_impl.h).
+//
+// Follows the arithmetic of reference src/attn.c:103-137: per query head h
+// (kv head h*n_kv/n_heads), scores s_t = (q_h . K_t) / sqrtf(d_head) over
+// t < seqlen, softmax, out_h = sum_t p_t V_t.  The positions of one session
+// and kv head are cut into splits of `split` positions; one work-group per
+// (kv head, split, vector) loads K/V for its split once and serves all G
+// query heads of the group.  Each split keeps (max, sum of exp, unnormalised
+// output); attn_merge_head combines the splits with the usual log-sum-exp
+// rescaling.  A session whose length fits one split is finished directly by
+// attn_split.
+#pragma once
+#include "common.h"
+#include "kernels.h"
+
+template <typename KT> struct KVec;   // 4 cache elements
+template <> struct KVec<float> { typedef float4 T; };
+template <> struct KVec<_Float16> { typedef f16x4 T; };
+
+template <typename KT>
+__device__ inline float4 to_f4(const typename KVec<KT>::T &v)
+{
+    if constexpr (sizeof(KT) == 4) return v;
+    else return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+
+// Split `sp` of `split` positions of one (kv head, vector), computed by a
+// work-group of NT threads: online softmax over chunks of CH = NT/4
+// positions.  The K and V of the next chunk are loaded while the current one
+// is reduced (K right after the scores, V right after the weighted sum).
+// Score phase: 4 threads per position, each a quarter of d_head
+// (interleaved 16-byte pieces, so a position's row is read contiguously).
+// Weighted-sum phase: thread (pg, dg) owns dims 4dg..4dg+3 and positions
+// p = pg (mod PG) of the chunk, for all G query heads.  Results leave
+// through the store policy M.
+template <int DH, typename KT, int NT, typename M>
+__device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, int n)
+{
+#pragma clang fp contract(off)
+    typedef typename KVec<KT>::T KV4;
+    constexpr int CH = NT / 4;                    // positions per chunk
+    constexpr int KQ = DH / 16;                   // 4-element pieces per thread (scores)
+    constexpr int DG = DH / 4, PG = NT / DG;
+    constexpr int VP = CH / PG;                   // positions per thread (weighted sum)
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int G = a.n_heads / a.n_kv;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int t0 = sp * a.split;
+    if (t0 >= L) return;
+    const int cnt = min(L, t0 + a.split) - t0;
+    const int nch = (cnt + CH - 1) / CH;
+    const int nact = (L + a.split - 1) / a.split;
+
+    __shared__ __attribute__((aligned(16))) float qsh[ATT_MAX_G][DH];
+    __shared__ float esh[ATT_MAX_G][CH];
+    __shared__ float alpha_sh[ATT_MAX_G], m_sh[ATT_MAX_G], l_sh[ATT_MAX_G];
+    __shared__ __attribute__((aligned(16))) float red[PG * ATT_MAX_G * DH];
+
+    const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
+    const KT *kb = (const KT *)a.kv.k_base + off;
+    const KT *vb = (const KT *)a.kv.v_base + off;
+
+    const int sp_p = tid >> 2, sj = tid & 3;      // score phase
+    const int dg = tid % DG, pg = tid / DG;       // weighted-sum phase
+    KV4 kr[KQ], vr[VP];
+    auto load_k = [&](int c) {
+        const int p = min(c * CH + sp_p, cnt - 1);
+#pragma unroll
+        for (int i = 0; i < KQ; i++) kr[i] = ldg((const KV4 *)(kb + (size_t)p * DH + 4 * (sj + 4 * i)));
+    };
+    auto load_v = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < VP; i++) {
+            const int p = min(c * CH + pg + PG * i, cnt - 1);
+            vr[i] = ldg((const KV4 *)(vb + (size_t)p * DH + 4 * dg));
+        }
+    };
+    load_k(0);
+    load_v(0);
+    const float *qn = a.q + (size_t)n * a.q_stride + (size_t)kvh * G * DH;
+    for (int i = tid; i < G * DH; i += NT) qsh[i / DH][i % DH] = *gptr(qn + i);
+    if (tid < ATT_MAX_G) {
+        m_sh[tid] = -INFINITY;
+        l_sh[tid] = 0.0f;
+    }
+    __syncthreads();
+
+    const float scale = 1.0f / sqrtf((float)DH);
+    float4 o[ATT_MAX_G];
+#pragma unroll
+    for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    for (int c = 0; c < nch; c++) {
+        const int ccnt = min(CH, cnt - c * CH);
+        // scores of this chunk
+        float dot[ATT_MAX_G];
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) dot[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KQ; i++) {
+            const float4 kv = to_f4<KT>(kr[i]);
+            const int d0 = 4 * (sj + 4 * i);
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++) {
+                if (h < G) {
+                    const float4 qv = *(const float4 *)&qsh[h][d0];
+                    dot[h] = fmaf(qv.x, kv.x, dot[h]);
+                    dot[h] = fmaf(qv.y, kv.y, dot[h]);
+                    dot[h] = fmaf(qv.z, kv.z, dot[h]);
+                    dot[h] = fmaf(qv.w, kv.w, dot[h]);
+                }
+            }
+        }
+        if (c + 1 < nch) load_k(c + 1);
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) {
+            dot[h] += __shfl_xor(dot[h], 1, 64);
+            dot[h] += __shfl_xor(dot[h], 2, 64);
+        }
+        if (sj == 0) {
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++)
+                if (h < G) esh[h][sp_p] = sp_p < ccnt ? dot[h] * scale : -INFINITY;
+        }
+        __syncthreads();
+        // online softmax: wave w owns heads w, w + NT/64, ...; lane j holds
+        // positions j, j + 64, ... of the chunk
+        for (int h = wid; h < G; h += NT / 64) {
+            float sv[CH / 64];
+            float mc = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < CH / 64; j++) {
+                sv[j] = esh[h][lane + 64 * j];
+                mc = fmaxf(mc, sv[j]);
+            }
+            mc = wave_max(mc);
+            const float mo = m_sh[h];
+            const float mn = fmaxf(mo, mc);
+            float ls = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CH / 64; j++) {
+                const float e = expf(sv[j] - mn);
+                esh[h][lane + 64 * j] = e;
+                ls += e;
+            }
+            ls = wave_sum(ls);
+            if (lane == 0) {
+                const float al = expf(mo - mn);
+                alpha_sh[h] = al;
+                m_sh[h] = mn;
+                l_sh[h] = l_sh[h] * al + ls;
+            }
+        }
+        __syncthreads();
+        // weighted sum of V
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) {
+            if (h < G) {
+                const float al = alpha_sh[h];
+                o[h].x *= al;
+                o[h].y *= al;
+                o[h].z *= al;
+                o[h].w *= al;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VP; i++) {
+            const int p = pg + PG * i;
+            const float4 v = to_f4<KT>(vr[i]);
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++) {
+                if (h < G) {
+                    const float e = esh[h][p];   // 0 past the chunk's end
+                    o[h].x = fmaf(e, v.x, o[h].x);
+                    o[h].y = fmaf(e, v.y, o[h].y);
+                    o[h].z = fmaf(e, v.z, o[h].z);
+                    o[h].w = fmaf(e, v.w, o[h].w);
+                }
+            }
+        }
+        if (c + 1 < nch) load_v(c + 1);
+        __syncthreads();   // esh / alpha are rewritten by the next chunk
+    }
+
+#pragma unroll
+    for (int h = 0; h < ATT_MAX_G; h++)
+        if (h < G) *(float4 *)&red[((size_t)pg * G + h) * DH + 4 * dg] = o[h];
+    __syncthreads();
+    const bool single = nact == 1;
+    const size_t sbase = (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G;
+    for (int i = tid; i < G * DH; i += NT) {
+        const int h = i / DH, d = i % DH;
+        float sum = 0.0f;
+        for (int q = 0; q < PG; q++) sum += red[((size_t)q * G + h) * DH + d];
+        if (single) {
+            const float ov = sum / l_sh[h];
+            const int k = (kvh * G + h) * DH + d;
+            if (a.out) M::st(a.out + (size_t)n * a.out_stride + k, ov);
+            if (a.next.q) act_put<M>(a.next, n, k, ov);
+        } else {
+            M::st(a.po + (sbase + h) * DH + d, sum);
+        }
+    }
+    if (!single && tid < G) {
+        M::st(a.pm + sbase + tid, m_sh[tid]);
+        M::st(a.pl + sbase + tid, l_sh[tid]);
+    }
+    __syncthreads();   // the LDS areas may be reused by the caller
+}
+
+// Merge of the splits of one (query head, vector) by NT threads:
+// mx = max_s m_s, L = sum_s l_s e^(m_s - mx), out = sum_s o_s e^(m_s - mx) / L.
+// Thread (d, sg) sums the splits s = sg (mod SG) for dim d; the SG partial
+// sums meet in LDS in a fixed order.  Sessions whose length fits one split
+// were finished by attn_split.
+template <int DH, int NT, typename M>
+__device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n)
+{
+    constexpr int SG = NT / DH;
+    const int tid = threadIdx.x;
+    const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int nact = (L + a.split - 1) / a.split;
+    if (nact <= 1) return;
+    __shared__ float wsh[ATT_MAX_MERGE];
+    __shared__ float rsh[NT / 64];
+    __shared__ float part[SG][DH];
+    const size_t hb = (((size_t)n * a.n_kv + kvh) * a.max_splits) * G + h;   // + s * G
+    const int w = tid >> 6, lane = tid & 63;
+    float mx = -INFINITY;
+    for (int s = tid; s < nact; s += NT) mx = fmaxf(mx, a.pm[hb + (size_t)s * G]);
+    mx = wave_max(mx);
+    if (lane == 0) rsh[w] = mx;
+    __syncthreads();
+    mx = rsh[0];
+    for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, rsh[i]);
+    float Ls = 0.0f;
+    for (int s = tid; s < nact; s += NT) {
+        const float e = expf(a.pm[hb + (size_t)s * G] - mx);
+        wsh[s] = e;
+        Ls += a.pl[hb + (size_t)s * G] * e;
+    }
+    Ls = wave_sum(Ls);
+    __syncthreads();   // everyone has read rsh (max)
+    if (lane == 0) rsh[w] = Ls;
+    __syncthreads();
+    float Lt = 0.0f;
+    for (int i = 0; i < NT / 64; i++) Lt += rsh[i];
+    const int d = tid % DH, sg = tid / DH;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int s = sg; s < nact; s += SG) acc += a.po[(hb + (size_t)s * G) * DH + d] * wsh[s];
+    part[sg][d] = acc;
+    __syncthreads();
+    if (tid < DH) {
+        float o = 0.0f;
+        for (int g = 0; g < SG; g++) o += part[g][tid];
+        o /= Lt;
+        const int k = hq * DH + tid;
+        if (a.out) M::st(a.out + (size_t)n * a.out_stride + k, o);
+        if (a.next.q) act_put<M>(a.next, n, k, o);
+    }
+    __syncthreads();   // the LDS areas may be reused by the caller
+}
+

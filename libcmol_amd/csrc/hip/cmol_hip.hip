@@ -21,7 +21,7 @@
 
 namespace {
 
-constexpr int E_OK = 0, E_OOM = -1, E_INVALID = -3, E_UNSUPPORTED = -4, E_ARGS = -6;
+constexpr int E_OK = 0, E_OOM = -1, E_INVALID = -3, E_UNSUPPORTED = -4, E_ARGS = -6, E_TRUNC = -8;
 constexpr size_t ALIGN = 256;
 // vectors per matvec/GEMM call (the operand preparation grid's y extent)
 constexpr int GEMM_MAX_N = 65535;
@@ -547,6 +547,44 @@ int pick_fold(int rows, int cols, int max_sessions)
     return f;
 }
 
+// k parts per tile for the persistent decode kernel, where a wave finishes
+// its tiles alone: the largest fold whose padding stays within nb/16 blocks
+// of the unfolded layout's (more, smaller tiles spread one matrix over the
+// launch's waves).
+int persist_fold(int cols)
+{
+    const int nb = cols / 32;
+    const int base = 4 * fold_quads(nb, 1);
+    for (int f = 8; f > 1; f >>= 1)
+        if (4 * f * fold_quads(nb, f) <= base + nb / 16) return f;
+    return 1;
+}
+
+// Layer weight format when the model's single session decodes with the
+// persistent kernel, else 0.  Opt-in with CMOL_PERSIST=1 in the environment
+// (one session, d_head 64 or 128, every layer matrix in one format): on
+// MI355X its device-wide barriers cost about as much as the kernel
+// boundaries of the decode graph they replace, and the graph stays faster.
+int persist_format(const cmolhip_model_desc_t *d)
+{
+    const char *e = getenv("CMOL_PERSIST");
+    if (!e || e[0] != '1') return 0;
+    const cmolhip_hparams_t &h = d->hp;
+    if (h.max_sessions != 1 || (h.d_head != 64 && h.d_head != 128)) return 0;
+    const int dt = d->layers[0].q.dtype;
+    for (int l = 0; l < h.n_layers; l++) {
+        const cmolhip_layer_tensors_t &L = d->layers[l];
+        if (L.q.dtype != dt || L.o.dtype != dt || L.gate.dtype != dt || L.down.dtype != dt) return 0;
+    }
+    return dt;
+}
+
+// Fold of a layer matrix (rows x cols) of model d.
+int layer_fold(const cmolhip_model_desc_t *d, int rows, int cols)
+{
+    return persist_format(d) ? persist_fold(cols) : pick_fold(rows, cols, d->hp.max_sessions);
+}
+
 } // namespace
 
 extern "C" int cmolhip_pick_fold(int rows, int cols, int max_sessions)
@@ -641,6 +679,48 @@ void plan_prefill(Plan &P, const cmolhip_hparams_t &h)
     P.add((size_t)cap * np * h.d_head * 4);
 }
 
+// Fold of the embedding / LM head (tied or not): the persistent kernel
+// spreads the LM head like the layer matrices.
+int head_fold(const cmolhip_model_desc_t *d) { return persist_format(d) ? persist_fold(d->hp.d_model) : 1; }
+
+// Attention splits of the persistent kernel's partial buffers.
+int persist_max_splits(int max_ctx) { return attn_max_splits(max_ctx, PK_CHUNK); }
+
+// CMOL_PERSIST_TRACE=1: the persistent kernel records when every
+// work-group has arrived at each barrier (profiling; see
+// cmolhip_persist_trace).
+bool persist_tracing()
+{
+    const char *e = getenv("CMOL_PERSIST_TRACE");
+    return e && e[0] == '1';
+}
+
+// Trace entries of one launch: start, one per barrier (at most 6 per layer
+// + 1), end.
+int pk_trace_cap(const cmolhip_hparams_t &h) { return 6 * h.n_layers + 3; }
+
+// Exchange buffers of the persistent kernel, in allocation order (mirrored
+// by build_persist).
+void plan_persist(Plan &P, const cmolhip_hparams_t &h)
+{
+    const size_t d = h.d_model, np = (size_t)h.n_heads * persist_max_splits(h.max_ctx);
+    for (int l = 0; l < h.n_layers; l++) {
+        for (int i = 0; i < 4; i++) P.add(d * 4);   // q, att, x_attn, x_ffn
+        P.add((size_t)h.d_ffn * 4);                 // h
+        P.add(np * 4);
+        P.add(np * 4);
+        P.add(np * h.d_head * 4);
+    }
+    P.add(d * 4);
+    P.add((size_t)h.n_layers * sizeof(PkLayer));
+    P.add((size_t)(16 * PK_MAX_WGS + 8 * 32) * 4);
+    P.add(4);
+    if (persist_tracing()) {
+        P.add((size_t)pk_trace_cap(h) * 8);
+        P.add((size_t)pk_trace_cap(h) * PK_MAX_WGS * 4 * 8);
+    }
+}
+
 Plan make_plan(const cmolhip_model_desc_t *d)
 {
     const cmolhip_hparams_t &h = d->hp;
@@ -662,16 +742,15 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(P.staging);
     for (int l = 0; l < h.n_layers; l++) {
         const auto &L = d->layers[l];
-        const int ms = h.max_sessions;
-        add_q(P, L.q.dtype, h.d_model + 2 * kvd, h.d_model, pick_fold(h.d_model + 2 * kvd, h.d_model, ms));
-        add_q(P, L.o.dtype, h.d_model, h.d_model, pick_fold(h.d_model, h.d_model, ms));
-        add_q(P, L.gate.dtype, 2 * h.d_ffn, h.d_model, pick_fold(2 * h.d_ffn, h.d_model, ms));
-        add_q(P, L.down.dtype, h.d_model, h.d_ffn, pick_fold(h.d_model, h.d_ffn, ms));
+        add_q(P, L.q.dtype, h.d_model + 2 * kvd, h.d_model, layer_fold(d, h.d_model + 2 * kvd, h.d_model));
+        add_q(P, L.o.dtype, h.d_model, h.d_model, layer_fold(d, h.d_model, h.d_model));
+        add_q(P, L.gate.dtype, 2 * h.d_ffn, h.d_model, layer_fold(d, 2 * h.d_ffn, h.d_model));
+        add_q(P, L.down.dtype, h.d_model, h.d_ffn, layer_fold(d, h.d_model, h.d_ffn));
         P.add((size_t)h.d_model * 4);
         P.add((size_t)h.d_model * 4);
     }
-    add_q(P, d->embd.dtype, h.vocab, h.d_model, 1);
-    if (d->lm_head.data) add_q(P, d->lm_head.dtype, h.vocab, h.d_model, 1);
+    add_q(P, d->embd.dtype, h.vocab, h.d_model, head_fold(d));
+    if (d->lm_head.data) add_q(P, d->lm_head.dtype, h.vocab, h.d_model, head_fold(d));
     P.add((size_t)h.d_model * 4);                                   // out_norm
     P.add((size_t)h.max_ctx * (h.d_head / 2) * 2 * 4);              // rope
     const size_t esz = h.kv_f16 ? 2 : 4;
@@ -682,6 +761,7 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     for (int s = 0; s < h.max_sessions; s++) plan_batch(P, h, 1, ms);
     plan_batch(P, h, h.max_sessions, ms);                           // lock-step batch
     plan_prefill(P, h);
+    if (persist_format(d)) plan_persist(P, h);
     return P;
 }
 
@@ -701,6 +781,13 @@ struct cmolhip_model {
     std::unique_ptr<Prefill> pf;                 // prompt passes
     std::mutex scratch_mu;
     bool use_graph = true;
+    // persistent single-session decode (pk_dt = layer format, 0: not used)
+    int pk_dt = 0, pk_nwg = 0, pk_lds = 0;
+    PkArgs pk{};                  // launch arguments but the per-step fields
+    unsigned pk_epoch = 0;        // barrier epochs used so far
+    int *h_pk_err = nullptr;      // pinned copy of pk.err
+    unsigned long long *h_trace = nullptr;   // pinned copy of the last step's stage times
+    int trace_n = 0;
 };
 
 namespace {
@@ -1020,6 +1107,146 @@ int build_prefill(cmolhip_model *m, Prefill &F)
     return E_OK;
 }
 
+int persist_capacity(int dt, int d_head, int kv_f16, int lds)
+{
+    switch (dt) {
+    case DT_Q4_0: return persist_capacity_q4(d_head, kv_f16, lds);
+    case DT_Q5_0: return persist_capacity_q5(d_head, kv_f16, lds);
+    case DT_Q8_0: return persist_capacity_q8(d_head, kv_f16, lds);
+    default: return 0;
+    }
+}
+
+int launch_persist(int dt, const PkArgs &a, int nwg, int lds, hipStream_t s)
+{
+    switch (dt) {
+    case DT_Q4_0: return launch_persist_q4(a, nwg, lds, s);
+    case DT_Q5_0: return launch_persist_q5(a, nwg, lds, s);
+    case DT_Q8_0: return launch_persist_q8(a, nwg, lds, s);
+    default: return E_UNSUPPORTED;
+    }
+}
+
+// Exchange buffers and launch arguments of the persistent kernel (after the
+// weights and caches exist).  The kernel stays off (pk_dt = 0) when the
+// device cannot keep a work-group per CU resident with its LDS needs.
+int build_persist(cmolhip_model *m, int dt)
+{
+    cmolhip_ctx_t *c = m->ctx;
+    const cmolhip_hparams_t &h = m->hp;
+    const size_t d = h.d_model, np = (size_t)h.n_heads * persist_max_splits(h.max_ctx);
+    std::vector<PkLayer> ly(h.n_layers);
+    int lds = 0;
+    auto need = [&](const cmolhip_qtensor_t &t) {
+        const int b = pk_gemv_lds(t.fold, t.block_quads);
+        lds = b > lds ? b : lds;
+    };
+    for (int l = 0; l < h.n_layers; l++) {
+        const MLayer &L = m->layers[l];
+        PkLayer &Y = ly[l];
+        Y.qkv = to_qt(L.qkv);
+        Y.o = to_qt(L.o);
+        Y.gu = to_qt(L.gu);
+        Y.down = to_qt(L.down);
+        need(L.qkv);
+        need(L.o);
+        need(L.gu);
+        need(L.down);
+        Y.attn_norm = L.attn_norm;
+        Y.ffn_norm = L.ffn_norm;
+        Y.rope_on = L.rope_on;
+        Y.kv_off = (size_t)l * m->layer_stride;
+        RC(arena_get(c, d, &Y.q));
+        RC(arena_get(c, d, &Y.att));
+        RC(arena_get(c, d, &Y.x_attn));
+        RC(arena_get(c, d, &Y.x_ffn));
+        RC(arena_get(c, (size_t)h.d_ffn, &Y.h));
+        RC(arena_get(c, np, &Y.pm));
+        RC(arena_get(c, np, &Y.pl));
+        RC(arena_get(c, np * h.d_head, &Y.po));
+    }
+    const cmolhip_qtensor_t &lm = lm_tensor(m);
+    need(lm);
+    PkArgs &a = m->pk;
+    a.n_layers = h.n_layers;
+    a.embd = to_qt(m->embd);
+    a.lm = to_qt(lm);
+    a.out_norm = m->out_norm;
+    a.rope = m->rope;
+    RC(arena_get(c, d, &a.x0));
+    PkLayer *dl = nullptr;
+    RC(cmolhip_alloc(c, ly.size() * sizeof(PkLayer), ALIGN, (void **)&dl));
+    RC(cmolhip_memcpy_h2d(c, dl, ly.data(), ly.size() * sizeof(PkLayer)));
+    a.layers = dl;
+    a.k_base = m->kbase;
+    a.v_base = m->vbase;
+    a.slot_stride = m->slot_stride;
+    a.d = h.d_model;
+    a.n_heads = h.n_heads;
+    a.n_kv = h.n_kv_heads;
+    a.d_head = h.d_head;
+    a.max_ctx = h.max_ctx;
+    a.kv_f16 = h.kv_f16;
+    a.max_splits = persist_max_splits(h.max_ctx);
+    a.eps = h.rms_eps;
+    const size_t sync_bytes = (size_t)(16 * PK_MAX_WGS + 8 * 32) * 4;
+    RC(cmolhip_alloc(c, sync_bytes, ALIGN, (void **)&a.sync));
+    RC(cmolhip_alloc(c, 4, ALIGN, (void **)&a.err));
+    HC(hipMemsetAsync(a.sync, 0, sync_bytes, c->stream));
+    HC(hipMemsetAsync(a.err, 0, 4, c->stream));
+    HC(hipHostMalloc((void **)&m->h_pk_err, 4, hipHostMallocDefault));
+    if (persist_tracing()) {
+        RC(arena_get(c, (size_t)pk_trace_cap(h), &a.trace));
+        RC(arena_get(c, (size_t)pk_trace_cap(h) * PK_MAX_WGS * 4, &a.marks));
+        HC(hipHostMalloc((void **)&m->h_trace, (size_t)pk_trace_cap(h) * 8, hipHostMallocDefault));
+    }
+    const int nwg = persist_capacity(dt, h.d_head, h.kv_f16, lds);
+    if (nwg < 1 || a.max_splits > ATT_MAX_MERGE) return E_OK;   // stays off
+    m->pk_dt = dt;
+    m->pk_nwg = nwg;
+    m->pk_lds = lds;
+    return E_OK;
+}
+
+// One decode step of the single session with the persistent kernel (the
+// step record is already on its way to B.steps on B.st).
+int run_persist(cmolhip_model *m, Batch &B)
+{
+    PkArgs a = m->pk;
+    a.step = B.steps;
+    a.slot_id = B.slot_ids;
+    a.logits = B.logits;
+    a.argmax = B.argmax;
+    const int L = B.h_steps[2] < m->hp.max_ctx ? B.h_steps[2] : m->hp.max_ctx;
+    const unsigned nb = (unsigned)pk_barriers(L, m->hp.n_kv_heads, m->pk_nwg, m->hp.n_layers);
+    if (m->pk_epoch > 0x7fffffffu) {   // restart the epochs long before they wrap
+        HC(hipMemsetAsync(a.sync, 0, (size_t)(16 * PK_MAX_WGS + 8 * 32) * 4, B.st));
+        m->pk_epoch = 0;
+    }
+    a.epoch0 = m->pk_epoch;
+    RC(launch_persist(m->pk_dt, a, m->pk_nwg, m->pk_lds, B.st));
+    m->pk_epoch += nb;
+    HC(hipMemcpyAsync(m->h_pk_err, a.err, 4, hipMemcpyDeviceToHost, B.st));
+    if (a.trace) {
+        m->trace_n = (int)nb + 2;
+        HC(hipMemcpyAsync(m->h_trace, a.trace, (size_t)m->trace_n * 8, hipMemcpyDeviceToHost, B.st));
+    }
+    return E_OK;
+}
+
+// After the step's synchronisation: a barrier wait that gave up leaves the
+// step's outputs invalid; the barrier state is reset for the next step.
+int persist_check(cmolhip_model *m, Batch &B)
+{
+    if (!*m->h_pk_err) return E_OK;
+    HC(hipMemsetAsync(m->pk.sync, 0, (size_t)(16 * PK_MAX_WGS + 8 * 32) * 4, B.st));
+    HC(hipMemsetAsync(m->pk.err, 0, 4, B.st));
+    HC(hipStreamSynchronize(B.st));
+    *m->h_pk_err = 0;
+    m->pk_epoch = 0;
+    return E_UNSUPPORTED;
+}
+
 int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
 {
     cmolhip_ctx_t *c = m->ctx;
@@ -1030,28 +1257,28 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &T = d->layers[l];
         MLayer &L = m->layers[l];
-        const int ms = h.max_sessions, kvd = h.n_kv_heads * h.d_head;
+        const int kvd = h.n_kv_heads * h.d_head;
         const cmolhip_host_tensor_t *qkv[3] = {&T.q, &T.k, &T.v};
-        RC(upload_q(c, 3, qkv, CMOLHIP_PARTS_CONCAT, pick_fold(h.d_model + 2 * kvd, h.d_model, ms),
+        RC(upload_q(c, 3, qkv, CMOLHIP_PARTS_CONCAT, layer_fold(d, h.d_model + 2 * kvd, h.d_model),
                     stg, P.staging, &L.qkv));
         const cmolhip_host_tensor_t *o[1] = {&T.o};
-        RC(upload_q(c, 1, o, CMOLHIP_PARTS_CONCAT, pick_fold(h.d_model, h.d_model, ms), stg,
+        RC(upload_q(c, 1, o, CMOLHIP_PARTS_CONCAT, layer_fold(d, h.d_model, h.d_model), stg,
                     P.staging, &L.o));
         const cmolhip_host_tensor_t *gu[2] = {&T.gate, &T.up};
-        RC(upload_q(c, 2, gu, CMOLHIP_PARTS_INTERLEAVE, pick_fold(2 * h.d_ffn, h.d_model, ms), stg,
+        RC(upload_q(c, 2, gu, CMOLHIP_PARTS_INTERLEAVE, layer_fold(d, 2 * h.d_ffn, h.d_model), stg,
                     P.staging, &L.gu));
         const cmolhip_host_tensor_t *dn[1] = {&T.down};
-        RC(upload_q(c, 1, dn, CMOLHIP_PARTS_CONCAT, pick_fold(h.d_model, h.d_ffn, ms), stg,
+        RC(upload_q(c, 1, dn, CMOLHIP_PARTS_CONCAT, layer_fold(d, h.d_model, h.d_ffn), stg,
                     P.staging, &L.down));
         RC(upload_norm(c, T.attn_norm, &L.attn_norm));
         RC(upload_norm(c, T.ffn_norm, &L.ffn_norm));
         L.rope_on = !(h.no_rope_interval > 0 && (l + 1) % h.no_rope_interval == 0);
     }
     const cmolhip_host_tensor_t *e[1] = {&d->embd};
-    RC(upload_q(c, 1, e, CMOLHIP_PARTS_CONCAT, 1, stg, P.staging, &m->embd));
+    RC(upload_q(c, 1, e, CMOLHIP_PARTS_CONCAT, head_fold(d), stg, P.staging, &m->embd));
     if (d->lm_head.data) {
         const cmolhip_host_tensor_t *lh[1] = {&d->lm_head};
-        RC(upload_q(c, 1, lh, CMOLHIP_PARTS_CONCAT, 1, stg, P.staging, &m->lm));
+        RC(upload_q(c, 1, lh, CMOLHIP_PARTS_CONCAT, head_fold(d), stg, P.staging, &m->lm));
     }
     RC(upload_norm(c, d->out_norm, &m->out_norm));
     const size_t rope_n = (size_t)h.max_ctx * (h.d_head / 2) * 2;
@@ -1079,6 +1306,7 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     RC(build_batch(m, *m->multi, h.max_sessions));
     m->pf.reset(new Prefill());
     RC(build_prefill(m, *m->pf));
+    if (persist_format(d)) RC(build_persist(m, persist_format(d)));
     HC(hipStreamSynchronize(c->stream));
     if (m->use_graph) {
         for (auto &sp : m->slots) {
@@ -1176,6 +1404,8 @@ void cmolhip_model_destroy(cmolhip_model_t *m)
         if (m->pf->h_steps) (void)hipHostFree(m->pf->h_steps);
         if (m->pf->h_slots) (void)hipHostFree(m->pf->h_slots);
     }
+    if (m->h_pk_err) (void)hipHostFree(m->h_pk_err);
+    if (m->h_trace) (void)hipHostFree(m->h_trace);
     cmolhip_ctx_destroy(m->ctx);
     delete m;
 }
@@ -1199,8 +1429,34 @@ int cmolhip_decode(cmolhip_model_t *m, int slot, int32_t token, int32_t pos, flo
     B.h_steps[1] = pos;
     B.h_steps[2] = pos + 1;
     HC(hipMemcpyAsync(B.steps, B.h_steps, 12, hipMemcpyHostToDevice, B.st));
+    if (m->pk_dt) {
+        RC(run_persist(m, B));
+        RC(finish(m, B, 1, logits_host, argmax));
+        return persist_check(m, B);
+    }
     RC(run_single(m, B));
     return finish(m, B, 1, logits_host, argmax);
+}
+
+int cmolhip_model_persistent(cmolhip_model_t *m) { return m && m->pk_dt ? 1 : 0; }
+
+int cmolhip_persist_marks(cmolhip_model_t *m, uint64_t *out, size_t cap)
+{
+    if (!m || !out) return E_ARGS;
+    if (!m->pk.marks || !m->trace_n) return 0;
+    const size_t n = (size_t)(m->trace_n - 1) * m->pk_nwg * 4;
+    if (cap < n) return E_TRUNC;
+    HC(hipMemcpy(out, m->pk.marks, n * 8, hipMemcpyDeviceToHost));
+    return m->pk_nwg;
+}
+
+int cmolhip_persist_trace(cmolhip_model_t *m, uint64_t *out, int cap)
+{
+    if (!m || !out || cap < 0) return E_ARGS;
+    if (!m->h_trace) return 0;
+    const int n = m->trace_n < cap ? m->trace_n : cap;
+    for (int i = 0; i < n; i++) out[i] = m->h_trace[i];
+    return n;
 }
 
 int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, int32_t pos0,

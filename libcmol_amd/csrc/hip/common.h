@@ -14,6 +14,31 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q5_0 = 6, DT_Q8_0 = 8 };
 
+// Global-memory view of a generic pointer: accesses through the result
+// compile to global_* instructions.  Used where the compiler cannot infer the
+// address space itself (pointers read from memory), which would otherwise
+// get flat_* accesses that also count against the LDS/scalar wait counter.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *gptr(const T *p)
+{
+    return (const __attribute__((address_space(1))) T *)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *gptr(T *p)
+{
+    return (__attribute__((address_space(1))) T *)p;
+}
+
+// Load of a 4-, 8- or 16-byte value (vector class types included) through
+// gptr.
+template <typename T>
+__device__ __forceinline__ T ldg(const T *p)
+{
+    if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, *gptr((const u32x4 *)p));
+    else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, *gptr((const u32x2 *)p));
+    else return __builtin_bit_cast(T, *gptr((const uint32_t *)p));
+}
+
 // ---------------------------------------------------------------------------
 // Tiled weight layout ("quad tiles").
 //

@@ -25,10 +25,11 @@ typedef __attribute__((address_space(3))) void lvoid_t;
 // expcnt 6:4, lgkmcnt 11:8)
 #define WAITCNT_VM_LGKM0(N) (((N) & 15) | (((N) >> 4) << 14) | (7 << 4))
 
+template <typename M = StPlain>
 __device__ inline void store_kv(void *base, int kv_f16, size_t idx, float v)
 {
-    if (kv_f16) ((_Float16 *)base)[idx] = (_Float16)v;
-    else ((float *)base)[idx] = v;
+    if (kv_f16) M::st((_Float16 *)base + idx, (_Float16)v);
+    else M::st((float *)base + idx, v);
 }
 
 // Sum / max over aligned groups of R lanes (R = 2, 4, 8 or 16).
@@ -94,60 +95,98 @@ __device__ inline void lds_zero(uint8_t *dst, int bytes, int tid)
     for (int off = tid * 16; off < bytes; off += NW * 64 * 16) *(u32x4 *)(dst + off) = u32x4{0, 0, 0, 0};
 }
 
+// Residual tail for row R*t + rl of vector v, x = residual + y already
+// formed: stores x, the next consumer's operand and the tile's sum of
+// squares.  Every lane of the wave calls it (shuffles in groups of R).
+template <typename M>
+__device__ __forceinline__ void resid_out(const GemvArgs &a, int t, int rl, int R, int v, bool act, float x)
+{
+#pragma clang fp contract(off)
+    const int row = t * R + rl;
+    if (act) {
+        M::st(a.out + (size_t)v * a.out_stride + row, x);
+        if (a.next.q) act_put<M>(a.next, v, row, x);
+    }
+    const float ss = group_sum(act ? x * x : 0.0f, R);
+    if (act && rl == 0 && a.next.ss) M::st(a.next.ss + (size_t)v * a.next.ss_stride + t, ss);
+}
+
+// Position of vector v for the QKV epilogue, clamped to the cache.
+__device__ __forceinline__ int epi_pos(const GemvArgs &a, int v)
+{
+    const int p = a.pos ? a.pos[(size_t)v * a.pos_stride] : a.pos0;
+    return min(max(p, 0), a.max_ctx - 1);
+}
+
+// RoPE (cos, sin) of QKV output row `row` at position pos (identity for
+// v rows or layers without RoPE).
+__device__ __forceinline__ float2 rope_cs(const GemvArgs &a, int row, int pos)
+{
+    if (!a.rope_on || row >= a.nq + a.nkv) return make_float2(1.0f, 0.0f);
+    const int rr = row < a.nq ? row : row - a.nq;
+    const auto *cs = gptr(a.rope + ((size_t)pos * (a.d_head / 2) + ((rr % a.d_head) >> 1)) * 2);
+    return make_float2(cs[0], cs[1]);
+}
+
+// QKV tail for row `row` of vector v: q rows (roped with cs) -> out, k rows
+// (roped) and v rows -> the KV cache at pos; `partner` is the pair's other
+// row (row ^ 1).
+template <typename M>
+__device__ __forceinline__ void qkv_out(const GemvArgs &a, int v, int row, float y, float partner, float2 cs, int pos)
+{
+#pragma clang fp contract(off)
+    const size_t kvo = kv_offset(a.kv, v);
+    if (row < a.nq + a.nkv) {
+        const int rr = row < a.nq ? row : row - a.nq;
+        const int i = rr % a.d_head;
+        float val = y;
+        if (a.rope_on) {
+            if (!(i & 1)) val = y * cs.x - partner * cs.y;
+            else val = partner * cs.y + y * cs.x;
+        }
+        if (row < a.nq) {
+            M::st(a.out + (size_t)v * a.out_stride + row, val);
+        } else {
+            const int h = rr / a.d_head;
+            store_kv<M>(a.kv.k_base, a.kv_f16, kvo + ((size_t)h * a.max_ctx + pos) * a.d_head + i, val);
+        }
+    } else {
+        const int rr = row - a.nq - a.nkv;
+        const int h = rr / a.d_head, i = rr % a.d_head;
+        store_kv<M>(a.kv.v_base, a.kv_f16, kvo + ((size_t)h * a.max_ctx + pos) * a.d_head + i, y);
+    }
+}
+
 // Epilogue for vector v, weight row R*t + rl.  Every lane of the wave calls
 // it (shuffles within aligned groups of R lanes, one group per (vector,
 // tile)); `act` marks lanes whose (row, v) is real.
-template <int EPI>
-__device__ void epilogue(const GemvArgs &a, int t, int rl, int R, int v, bool act, float y)
+template <int EPI, typename M = StPlain>
+__device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R, int v, bool act, float y)
 {
 #pragma clang fp contract(off)
     const int row = t * R + rl;
     act = act && row < a.w.rows;
     if constexpr (EPI == EPI_STORE) {
-        if (act) a.out[(size_t)v * a.out_stride + row] = y;
+        if (act) M::st(a.out + (size_t)v * a.out_stride + row, y);
     } else if constexpr (EPI == EPI_RESID) {
         float x = 0.0f;
         if (act) {
-            x = a.out[(size_t)v * a.out_stride + row] + y;
-            a.out[(size_t)v * a.out_stride + row] = x;
-            if (a.next.q) act_put(a.next, v, row, x);
+            const size_t i = (size_t)v * a.out_stride + row;
+            x = (a.res ? a.res[i] : a.out[i]) + y;
         }
-        const float ss = group_sum(x * x, R);
-        if (act && rl == 0 && a.next.ss) a.next.ss[(size_t)v * a.next.ss_stride + t] = ss;
+        resid_out<M>(a, t, rl, R, v, act, x);
     } else if constexpr (EPI == EPI_SWIGLU) {
         const float u = __shfl_xor(y, 1, 64);
         if (act && !(row & 1)) {
             const float h = (y / (1.0f + expf(-y))) * u;
-            if (a.out) a.out[(size_t)v * a.out_stride + (row >> 1)] = h;
-            if (a.next.q) act_put(a.next, v, row >> 1, h);
+            if (a.out) M::st(a.out + (size_t)v * a.out_stride + (row >> 1), h);
+            if (a.next.q) act_put<M>(a.next, v, row >> 1, h);
         }
     } else if constexpr (EPI == EPI_QKV) {
         const float partner = __shfl_xor(y, 1, 64);
         if (act) {
-            const int pos = min(max(a.pos[(size_t)v * a.pos_stride], 0), a.max_ctx - 1);
-            if (row < a.nq + a.nkv) {
-                const int rr = row < a.nq ? row : row - a.nq;
-                const int i = rr % a.d_head;
-                float val = y;
-                if (a.rope_on) {
-                    const float *cs = a.rope + ((size_t)pos * (a.d_head / 2) + (i >> 1)) * 2;
-                    const float c = cs[0], sn = cs[1];
-                    if (!(i & 1)) val = y * c - partner * sn;
-                    else val = partner * sn + y * c;
-                }
-                if (row < a.nq) {
-                    a.out[(size_t)v * a.out_stride + row] = val;
-                } else {
-                    const int h = rr / a.d_head;
-                    store_kv(a.kv.k_base, a.kv_f16,
-                             kv_offset(a.kv, v) + ((size_t)h * a.max_ctx + pos) * a.d_head + i, val);
-                }
-            } else {
-                const int rr = row - a.nq - a.nkv;
-                const int h = rr / a.d_head, i = rr % a.d_head;
-                store_kv(a.kv.v_base, a.kv_f16,
-                         kv_offset(a.kv, v) + ((size_t)h * a.max_ctx + pos) * a.d_head + i, y);
-            }
+            const int pos = epi_pos(a, v);
+            qkv_out<M>(a, v, row, y, partner, rope_cs(a, row, pos), pos);
         }
     } else if constexpr (EPI == EPI_LOGITS) {
         if (act) a.out[(size_t)v * a.out_stride + row] = y;

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.h"
+
 // Device view of a quad-tiled quantised tensor (see common.h).
 struct QTensor {
     uint8_t *qs;
@@ -15,7 +17,8 @@ struct QTensor {
 
 // KV caches of one layer for a batch of activation vectors: vector n uses
 // slot slot_ids[n], whose K cache starts at k_base + slot*slot_stride +
-// layer_off elements (fp32 or fp16 per kv_f16).
+// layer_off elements (fp32 or fp16 per kv_f16); without slot_ids every
+// vector uses k_base + layer_off.
 struct KVRef {
     void *k_base, *v_base;
     size_t slot_stride, layer_off;
@@ -24,7 +27,7 @@ struct KVRef {
 
 __device__ inline size_t kv_offset(const KVRef &r, int n)
 {
-    return (size_t)r.slot_ids[n] * r.slot_stride + r.layer_off;
+    return (r.slot_ids ? (size_t)r.slot_ids[n] * r.slot_stride : 0) + r.layer_off;
 }
 
 // ---------------------------------------------------------------------------
@@ -49,6 +52,31 @@ __device__ inline size_t kv_offset(const KVRef &r, int n)
 #define ACT_INV_SCALE 256.0f
 #define LO_SCALE 2048.0f
 #define LO_INV_SCALE (1.0f / 2048.0f)
+
+// ---------------------------------------------------------------------------
+// Store policies.  Plain stores suffice when a kernel boundary separates a
+// producer from its consumers.  Inside the persistent decode kernel a value
+// written by one work-group is read by others after a device-wide barrier,
+// possibly on another XCD, whose L2 is not coherent with the writer's: those
+// stores are relaxed agent-scope atomic stores (sc1: written through to
+// memory).  Every buffer that kernel hands over is written once per launch
+// before any work-group reads it, so the loads stay plain.
+// ---------------------------------------------------------------------------
+struct StPlain {
+    template <typename T> __device__ static void st(T *p, T v) { *p = v; }
+};
+struct StDev {
+    __device__ static void st(float *p, float v)
+    {
+        __hip_atomic_store(gptr((uint32_t *)p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __device__ static void st(_Float16 *p, _Float16 v)
+    {
+        __hip_atomic_store(gptr((uint16_t *)p), __builtin_bit_cast(uint16_t, v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+};
 
 struct ActOut {
     _Float16 *q;            // operand buffer of the consumer
@@ -96,14 +124,15 @@ struct GemvArgs {
     ActIn in;
     float *out;             // epilogue output [n][out_stride]
     int out_stride;
+    const float *res;       // EPI_RESID: residual input [n][out_stride] (nullptr: out itself)
     int n;                  // activation vectors
     ActOut next;            // EPI_RESID / EPI_SWIGLU: operand of the consumer
     // EPI_QKV
     int nq, nkv, d_head, max_ctx, kv_f16, rope_on;
     const float *rope;      // [max_ctx][d_head/2][2]
     KVRef kv;
-    const int32_t *pos;     // per-vector position, pos[n * pos_stride]
-    int pos_stride;
+    const int32_t *pos;     // per-vector position, pos[n * pos_stride] (nullptr: pos0)
+    int pos_stride, pos0;
     // EPI_LOGITS
     unsigned long long *argmax;   // ARGMAX_SLOTS slots per vector
     // when set, recorded at the kernel's own start and end (kernel timing)
@@ -120,6 +149,9 @@ int launch_act_prep(const float *x, int x_stride, int K, int n, const ActOut &o,
 size_t act_bytes(int K, int n);
 
 // ---- attn.hip
+#define ATT_MAX_G 8          // query heads per kv head
+#define ATT_MAX_MERGE 1024   // splits one merge can combine
+
 struct AttnArgs {
     const float *q;         // [n][n_heads*d_head]
     int q_stride;
@@ -138,6 +170,84 @@ struct AttnArgs {
 int launch_attn(const AttnArgs &a, hipStream_t s);
 int attn_max_splits(int max_ctx, int split);
 
+// ---- persist_q4/q5/q8.hip: the persistent single-session decode kernel
+#define PK_THREADS 512
+#define PK_WAVES (PK_THREADS / 64)
+#define PK_CHUNK (PK_THREADS / 4)   // attention positions per chunk
+#define PK_SPIN_MAX (1 << 18)       // polls of one barrier wait before it gives up
+#define PK_MAX_WGS 1024
+
+// Weights and exchange buffers of one layer (device copy, read-only).  The
+// stages hand each other plain fp32 vectors; every matvec stage builds its
+// own MFMA operand (and RMSNorm scale) from the vector it consumes.
+struct PkLayer {
+    QTensor qkv, o, gu, down;
+    const float *attn_norm, *ffn_norm;
+    int rope_on;
+    size_t kv_off;                 // layer offset in the KV caches (elements)
+    float *q;                      // roped queries [d]
+    float *att;                    // attention output [d]
+    float *x_attn, *x_ffn;         // residual after the attention block / after the FFN [d]
+    float *h;                      // SwiGLU output [d_ffn]
+    float *pm, *pl, *po;           // attention split partials
+};
+
+struct PkArgs {
+    const PkLayer *layers;
+    int n_layers;
+    QTensor embd, lm;
+    const float *out_norm, *rope;
+    float *x0;                     // embedding row [d]
+    float *logits;                 // [vocab]
+    unsigned long long *argmax;    // [ARGMAX_SLOTS]
+    void *k_base, *v_base;
+    size_t slot_stride;
+    const int32_t *slot_id;        // device [1]: the session's KV slot
+    const int32_t *step;           // device {token, pos, seqlen}
+    int d, n_heads, n_kv, d_head, max_ctx, kv_f16, max_splits;
+    float eps;
+    unsigned *sync;                // arrival words [PK_MAX_WGS][16], release words [8][32]
+    unsigned epoch0;               // barrier epochs of this launch are epoch0+1, epoch0+2, ...
+    int *err;                      // set when a barrier wait gave up
+    unsigned long long *trace;     // optional: [0] launch start, [i] all arrived at barrier i, then end
+    unsigned long long *marks;     // optional: [barrier i][work-group][4] phase times of stage i+1
+};
+
+// Positions per attention split for attended length L: multiples of the
+// chunk, enough splits to give every work-group an item.
+__host__ __device__ inline int pk_split(int L, int n_kv, int nwg)
+{
+    const int want = (L * n_kv + nwg - 1) / nwg;
+    const int s = (want + PK_CHUNK - 1) / PK_CHUNK * PK_CHUNK;
+    return s < PK_CHUNK ? PK_CHUNK : s;
+}
+
+// Barriers one launch passes: after the embedding, then per layer after the
+// QKV, attention, (merge,) Wo, gate/up and down stages.
+__host__ __device__ inline int pk_barriers(int L, int n_kv, int nwg, int n_layers)
+{
+    const int split = pk_split(L, n_kv, nwg);
+    const int nsplit = (L + split - 1) / split;
+    return 1 + n_layers * (5 + (nsplit > 1 ? 1 : 0));
+}
+
+// LDS bytes pk_gemv needs for a matrix (operand incl. padding blocks, a zero
+// slot, 16 floats of tile scratch per wave and the waves' sums of squares).
+__host__ __device__ inline int pk_gemv_lds(int fold, int block_quads)
+{
+    return 4 * fold * block_quads * 128 + 16 + PK_WAVES * 64 + PK_WAVES * 4;
+}
+
+// Launch (cooperative, nwg work-groups, lds dynamic LDS bytes) for layer
+// format q4/q5/q8; 0, -4 unsupported shape, -5 launch failure.
+int launch_persist_q4(const PkArgs &a, int nwg, int lds, hipStream_t s);
+int launch_persist_q5(const PkArgs &a, int nwg, int lds, hipStream_t s);
+int launch_persist_q8(const PkArgs &a, int nwg, int lds, hipStream_t s);
+// Work-groups such a launch keeps resident (0: it cannot run here).
+int persist_capacity_q4(int d_head, int kv_f16, int lds);
+int persist_capacity_q5(int d_head, int kv_f16, int lds);
+int persist_capacity_q8(int d_head, int kv_f16, int lds);
+
 // ---- misc.hip
 int launch_kv_synth(void *kc, void *vc, int n_kv, int max_ctx, int d_head,
                     int n_tokens, int kv_f16, uint64_t seed, hipStream_t s);
@@ -151,6 +261,7 @@ int launch_act_extract(const _Float16 *src, int K, int n, int v, _Float16 *dst, 
                        int ss_stride, int ss_count, float *ss_dst, hipStream_t s);
 
 // Writes value v of input k of vector n into an operand (see ActOut).
+template <typename M = StPlain>
 __device__ inline void act_put(const ActOut &o, int n, int k, float v)
 {
 #pragma clang fp contract(off)
@@ -169,6 +280,6 @@ __device__ inline void act_put(const ActOut &o, int n, int k, float v)
         e = hi16 * 4 + (j == 1 ? 2 : j == 2 ? 1 : j);
     }
     const size_t base = (((size_t)b * 4 + g) * o.nrows + 2 * n) * 8 + e;
-    o.q[base] = hi;
-    o.q[base + 8] = lo;
+    M::st(o.q + base, hi);
+    M::st(o.q + base + 8, lo);
 }

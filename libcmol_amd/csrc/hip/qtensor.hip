@@ -1,25 +1,6 @@
 // qtensor.hip — upload-time repack of GGUF blocks into the quad-tile layout,
 // bit-exact dequantisation from that layout, and the embedding-row gather.
-#include "common.h"
-#include "kernels.h"
-
-// Position of a destination tensor element in the tiled layout.
-struct CellPos {
-    size_t cell;   // t * BQ + q
-    int col;       // MFMA column 0..15
-    int bi;        // block within the quad
-};
-
-__device__ inline CellPos cell_pos(const QTensor &t, int row, int b)
-{
-    const int R = 16 / t.fold, BQ = t.block_quads;
-    const int part = b / (4 * BQ), bq = b - part * 4 * BQ;
-    CellPos p;
-    p.cell = (size_t)(row / R) * BQ + (bq >> 2);
-    p.col = part * R + row % R;
-    p.bi = bq & 3;
-    return p;
-}
+#include "qtensor_impl.h"
 
 // The lane's share of one GGUF block: codes (LB/4 bytes) and, for Q5_0, the
 // byte of fifth bits in the pair order deq_q5 expects (bit p = fifth bit of
@@ -127,23 +108,6 @@ int launch_repack(const QTensor &t, const uint8_t *raw, int rows, int row0,
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-// Decoded values of lane group g of one block (8 floats, written at their
-// natural k positions), computed through the same lane decoders the matvec
-// uses, times the fp32 scale.
-template <int DT>
-__device__ void block_values_g(const QTensor &t, int row, int b, int g, float *dst)
-{
-    constexpr int LB = QFmt<DT>::LANE_BYTES;
-    const CellPos cp = cell_pos(t, row, b);
-    const float d = f16_bits_to_f32(t.d[cp.cell * 64 + cp.col * 4 + cp.bi]);
-    const int lane = g * 16 + cp.col;
-    const u32x4 *p = (const u32x4 *)(t.qs + (cp.cell * 64 + lane) * LB);
-    const u32x4 c0 = p[0], c1 = LB == 32 ? p[1] : u32x4{0, 0, 0, 0};
-    const uint32_t h = DT == DT_Q5_0 ? t.qh[cp.cell * 64 + lane] : 0u;
-    const f16x8 v = deq_block<DT>(c0, c1, h, cp.bi);
-    for (int e = 0; e < 8; e++) dst[kmap(DT, g, e)] = mul_scale_x86(d, (float)v[e]);
-}
-
 template <int DT>
 __device__ void block_values(const QTensor &t, int row, int b, float *dst)
 {
@@ -184,30 +148,12 @@ __global__ __launch_bounds__(256) void k_embed(QTensor t, const int32_t *__restr
                                                int x_stride, ActOut o,
                                                unsigned long long *__restrict__ argmax, int n)
 {
-#pragma clang fp contract(off)
     const int s = blockIdx.y;
     if (s >= n) return;
-    const int nb = t.cols / 32;
-    int tok = token[s * token_stride];
+    const int tok = token[s * token_stride];
     if (argmax && blockIdx.x == 0)
         for (int i = threadIdx.x; i < ARGMAX_SLOTS; i += blockDim.x) argmax[(size_t)s * ARGMAX_SLOTS + i] = 0ull;
-    if (tok < 0 || tok >= t.rows) tok = 0;
-    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
-    const int b = gid >> 2, g = gid & 3;
-    float ss = 0.0f;
-    if (b < nb) {
-        float *xb = x + (size_t)s * x_stride + (size_t)b * 32;
-        block_values_g<DT>(t, tok, b, g, xb);
-        for (int e = 0; e < 8; e++) {
-            const int k = kmap(DT, g, e);
-            ss += xb[k] * xb[k];
-            if (o.q) act_put(o, s, 32 * b + k, xb[k]);
-        }
-    }
-    // per-block sum over the 4 lane groups (lanes 4b..4b+3 of the wave)
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
-    if (b < nb && g == 0 && o.ss) o.ss[(size_t)s * o.ss_stride + b] = ss;
+    embed_group<DT, StPlain>(t, tok, blockIdx.x * blockDim.x + threadIdx.x, x + (size_t)s * x_stride, o, s);
 }
 
 int launch_embed(const QTensor &t, const int32_t *token, int token_stride, float *x,

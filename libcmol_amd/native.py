@@ -104,6 +104,9 @@ SIGNATURES = [
     ("cmolhip_kv_upload", C.c_int, [P, C.c_int, C.c_int, C.c_int, P, P]),
     ("cmolhip_kv_fill_synthetic", C.c_int, [P, C.c_int, C.c_int, C.c_uint64]),
     ("cmolhip_session_stream", P, [P, C.c_int]),
+    ("cmolhip_model_persistent", C.c_int, [P]),
+    ("cmolhip_persist_trace", C.c_int, [P, P, C.c_int]),
+    ("cmolhip_persist_marks", C.c_int, [P, P, C.c_size_t]),
     # cmol_ext.h
     ("cmol__forward", C.c_int, [P, I32, C.c_int, P]),
     ("cmol__prefill", C.c_int, [P, P, C.c_int, P]),
@@ -277,6 +280,11 @@ class Model:
     @property
     def device(self):
         return lib().cmol__device(self.h)
+
+    @property
+    def persistent(self) -> bool:
+        """Single-session decode runs the persistent kernel."""
+        return bool(lib().cmolhip_model_persistent(self.device))
 
 
 class Session:
