@@ -255,7 +255,7 @@ def main():
     mv = []
     if "matvec" not in skip:
         for rows, cols in ((11008, 2048), (2048, 11008)):
-            for n in (1, 8):
+            for n in (1, 8, 32):
                 r = bench_matvec(rows, cols, n, copies=64, launches=256)
                 log(json.dumps(r))
                 mv.append(r)

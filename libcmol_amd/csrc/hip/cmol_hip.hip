@@ -310,6 +310,7 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
                                 void *ev_stop)
 {
     if (!c || !w || !op || !dy || n < 1 || n > GEMM_MAX_N || (!ev_start != !ev_stop)) return E_ARGS;
+    const size_t mark = arena_mark(c);
     GemvArgs a{};
     a.w = to_qt(*w);
     a.in.q = (const _Float16 *)op;
@@ -324,8 +325,14 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
     a.ev_start = (hipEvent_t)ev_start;
     a.ev_stop = (hipEvent_t)ev_stop;
     // up to 32 vectors stream the weights once through the matvec; more go
-    // to the tiled MFMA GEMM
-    return n <= 32 ? launch_gemv(a, EPI_STORE, c->stream) : launch_gemm(a, EPI_STORE, c->stream);
+    // to the tiled MFMA GEMM.  The arena space of k-split partial sums is
+    // released at once: later work on this stream runs after the kernels.
+    int rc = E_OK;
+    const size_t pf = n <= 32 ? gemv_part_floats(a.w, n) : 0;
+    if (pf) rc = arena_get(c, pf, &a.part);
+    if (rc == E_OK) rc = n <= 32 ? launch_gemv(a, EPI_STORE, c->stream) : launch_gemm(a, EPI_STORE, c->stream);
+    arena_release(c, mark);
+    return rc;
 }
 
 int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx, float *dy, int n,
@@ -455,6 +462,7 @@ struct Batch {
     float *ss_a = nullptr, *ss_b = nullptr;   // sum-of-squares partials [cap][d]
     unsigned long long *argmax = nullptr;     // [cap][ARGMAX_SLOTS]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
+    float *part = nullptr;                    // k-split partial sums of batched matvecs
     int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
     unsigned long long *h_argmax = nullptr;   // pinned [cap][ARGMAX_SLOTS]
@@ -635,9 +643,58 @@ int validate_desc(const cmolhip_model_desc_t *d)
     return E_OK;
 }
 
-// Buffers of one batch, in allocation order (mirrored by build_batch).
-void plan_batch(Plan &P, const cmolhip_hparams_t &h, int cap, int ms)
+// Fold of the embedding / LM head (tied or not): the persistent kernel
+// spreads the LM head like the layer matrices.
+int head_fold(const cmolhip_model_desc_t *d) { return persist_format(d) ? persist_fold(d->hp.d_model) : 1; }
+
+// Device view of the dimensions of a tiled tensor (no data), enough for
+// gemv_part_floats.
+QTensor shape_qt(int dt, int rows, int cols, int fold)
 {
+    QTensor t{};
+    t.dtype = dt;
+    t.rows = rows;
+    t.cols = cols;
+    t.fold = fold;
+    t.row_tiles = (rows + 16 / fold - 1) / (16 / fold);
+    t.block_quads = fold_quads(cols / 32, fold);
+    return t;
+}
+
+// Largest k-split scratch any matvec of a batch of up to cap vectors of
+// model d needs (the split count depends on the batch size).
+size_t batch_part_floats(const cmolhip_model_desc_t *d, int cap)
+{
+    const cmolhip_hparams_t &h = d->hp;
+    const int kvd = h.n_kv_heads * h.d_head;
+    size_t m = 0;
+    auto upd = [&](int dt, int rows, int cols) {
+        const QTensor t = shape_qt(dt, rows, cols, layer_fold(d, rows, cols));
+        for (int n = 1; n <= cap; n++) {
+            const size_t f = gemv_part_floats(t, n);
+            m = f > m ? f : m;
+        }
+    };
+    for (int l = 0; l < h.n_layers; l++) {
+        const cmolhip_layer_tensors_t &L = d->layers[l];
+        upd(L.q.dtype, h.d_model + 2 * kvd, h.d_model);
+        upd(L.o.dtype, h.d_model, h.d_model);
+        upd(L.gate.dtype, 2 * h.d_ffn, h.d_model);
+        upd(L.down.dtype, h.d_model, h.d_ffn);
+    }
+    const cmolhip_host_tensor_t &lm = d->lm_head.data ? d->lm_head : d->embd;
+    const QTensor t = shape_qt(lm.dtype, h.vocab, h.d_model, head_fold(d));
+    for (int n = 1; n <= cap; n++) {
+        const size_t f = gemv_part_floats(t, n);
+        m = f > m ? f : m;
+    }
+    return m;
+}
+
+// Buffers of one batch, in allocation order (mirrored by build_batch).
+void plan_batch(Plan &P, const cmolhip_model_desc_t *d, int cap, int ms)
+{
+    const cmolhip_hparams_t &h = d->hp;
     const size_t np = (size_t)h.n_kv_heads * ms * (h.n_heads / h.n_kv_heads);
     P.add((size_t)cap * 3 * 4);
     P.add((size_t)cap * 4);
@@ -655,6 +712,7 @@ void plan_batch(Plan &P, const cmolhip_hparams_t &h, int cap, int ms)
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * h.d_head * 4);
+    P.add(batch_part_floats(d, cap) * 4);
 }
 
 // Buffers of the prompt pass, in allocation order (mirrored by build_prefill).
@@ -679,9 +737,6 @@ void plan_prefill(Plan &P, const cmolhip_hparams_t &h)
     P.add((size_t)cap * np * h.d_head * 4);
 }
 
-// Fold of the embedding / LM head (tied or not): the persistent kernel
-// spreads the LM head like the layer matrices.
-int head_fold(const cmolhip_model_desc_t *d) { return persist_format(d) ? persist_fold(d->hp.d_model) : 1; }
 
 // Attention splits of the persistent kernel's partial buffers.
 int persist_max_splits(int max_ctx) { return attn_max_splits(max_ctx, PK_CHUNK); }
@@ -758,8 +813,8 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(kv_elems * esz);
     P.add(kv_elems * esz);
     P.add((size_t)h.n_kv_heads * h.max_ctx * h.d_head * 4);         // scratch
-    for (int s = 0; s < h.max_sessions; s++) plan_batch(P, h, 1, ms);
-    plan_batch(P, h, h.max_sessions, ms);                           // lock-step batch
+    for (int s = 0; s < h.max_sessions; s++) plan_batch(P, d, 1, ms);
+    plan_batch(P, d, h.max_sessions, ms);                           // lock-step batch
     plan_prefill(P, h);
     if (persist_format(d)) plan_persist(P, h);
     return P;
@@ -861,6 +916,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         g.kv = kvref(m, B, l);
         g.pos = B.steps + 1;
         g.pos_stride = 3;
+        g.part = B.part;
         RC(launch_gemv(g, EPI_QKV, st));
 
         AttnArgs at{};
@@ -891,6 +947,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         go.out_stride = d;
         go.n = n;
         go.next = act_out(B.op_gu, L.gu.dtype, n, L.ffn_norm, B.ss_b, P);
+        go.part = B.part;
         RC(launch_gemv(go, EPI_RESID, st));
 
         GemvArgs gu{};
@@ -899,6 +956,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         gu.out = nullptr;
         gu.n = n;
         gu.next = act_out(B.op_dn, L.down.dtype, n, nullptr, nullptr, 0);
+        gu.part = B.part;
         RC(launch_gemv(gu, EPI_SWIGLU, st));
 
         GemvArgs gd{};
@@ -911,6 +969,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
             gd.next = act_out(B.op_qkv, m->layers[l + 1].qkv.dtype, n, m->layers[l + 1].attn_norm, B.ss_a, P);
         else
             gd.next = act_out(B.op_lm, lm_tensor(m).dtype, n, m->out_norm, B.ss_a, P);
+        gd.part = B.part;
         RC(launch_gemv(gd, EPI_RESID, st));
         ss_count = L.down.row_tiles;
     }
@@ -921,6 +980,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
     gl.out_stride = hp.vocab;
     gl.n = n;
     gl.argmax = B.argmax;
+    gl.part = B.part;
     RC(launch_gemv(gl, EPI_LOGITS, st));
     return E_OK;
 }
@@ -1050,7 +1110,7 @@ int upload_q(cmolhip_ctx_t *c, int n, const cmolhip_host_tensor_t *const *ts, in
     return cmolhip_qtensor_upload(c, ts[0]->dtype, ts[0]->cols, fold, n, parts, rows, mode, stg, stg_bytes, out);
 }
 
-int build_batch(cmolhip_model *m, Batch &B, int cap)
+int build_batch(cmolhip_model *m, Batch &B, int cap, size_t part_floats)
 {
     cmolhip_ctx_t *c = m->ctx;
     const cmolhip_hparams_t &h = m->hp;
@@ -1073,6 +1133,7 @@ int build_batch(cmolhip_model *m, Batch &B, int cap)
     RC(arena_get(c, (size_t)cap * np, &B.pm));
     RC(arena_get(c, (size_t)cap * np, &B.pl));
     RC(arena_get(c, (size_t)cap * np * h.d_head, &B.po));
+    if (part_floats) RC(arena_get(c, part_floats, &B.part));
     HC(hipMemsetAsync(B.steps, 0, (size_t)cap * 12, c->stream));
     HC(hipStreamCreateWithFlags(&B.st, hipStreamNonBlocking));
     HC(hipHostMalloc((void **)&B.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
@@ -1298,12 +1359,12 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     for (int s = 0; s < h.max_sessions; s++) {
         m->slots.emplace_back(new Batch());
         Batch &B = *m->slots.back();
-        RC(build_batch(m, B, 1));
+        RC(build_batch(m, B, 1, batch_part_floats(d, 1)));
         const int32_t sid = s;
         RC(cmolhip_memcpy_h2d(c, B.slot_ids, &sid, 4));
     }
     m->multi.reset(new Batch());
-    RC(build_batch(m, *m->multi, h.max_sessions));
+    RC(build_batch(m, *m->multi, h.max_sessions, batch_part_floats(d, h.max_sessions)));
     m->pf.reset(new Prefill());
     RC(build_prefill(m, *m->pf));
     if (persist_format(d)) RC(build_persist(m, persist_format(d)));

@@ -21,8 +21,7 @@
 //            SwiGLU over interleaved gate/up rows [src/model.c:117-123];
 //            RoPE on q/k rows + KV-cache write at pos [src/attn.c:83-101];
 //            logits + first-index argmax [src/sampler.c:199-204].
-#include "common.h"
-#include "kernels.h"
+#include "gemv_impl.h"
 
 int launch_gemv_q4(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemv_q5(const GemvArgs &a, int epi, hipStream_t s);
@@ -64,6 +63,55 @@ int launch_gemm(const GemvArgs &a, int epi, hipStream_t s)
     }
     if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+size_t gemv_part_floats(const QTensor &w, int n)
+{
+    if (n <= GB_VG || w.fold != 1) return 0;
+    GbShape sh;
+    gb_plan(w, n, sh);
+    return sh.splits > 1 ? (size_t)sh.splits * n * w.rows : 0;
+}
+
+// k-split finish: one wave per (64 rows, vector); lane l takes row 64*bx + l,
+// so the lanes of a 16-row tile are a 16-lane group, as the epilogues need.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, int ss_count)
+{
+#pragma clang fp contract(off)
+    const int v = blockIdx.y, l = threadIdx.x & 63;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + l;
+    if ((row & ~63) >= a.w.rows) return;   // whole waves past the matrix
+    float nrm = 1.0f;
+    if (ss_count) {
+        float s = 0.0f;
+        for (int i = l; i < ss_count; i += 64) s += a.in.ss[(size_t)v * a.in.ss_stride + i];
+        s = wave_sum(s);
+        nrm = 1.0f / sqrtf(s / (float)a.w.cols + a.in.eps);
+    }
+    const bool act = row < a.w.rows;
+    float y = 0.0f;
+    if (act)
+        for (int k = 0; k < splits; k++) y += a.part[((size_t)k * a.n + v) * a.w.rows + row];
+    y *= nrm;
+    epilogue<EPI>(a, row >> 4, row & 15, 16, v, act, y);
+}
+
+int launch_gemv_b_finish(const GemvArgs &a, int epi, int splits, int ss_count, hipStream_t s)
+{
+    const dim3 grid((a.w.rows + 255) / 256, a.n), block(256);
+    auto go = [&](auto kern) {
+        if (a.ev_stop) hipExtLaunchKernelGGL(kern, grid, block, 0, s, nullptr, a.ev_stop, 0, a, splits, ss_count);
+        else hipLaunchKernelGGL(kern, grid, block, 0, s, a, splits, ss_count);
+    };
+    switch (epi) {
+    case EPI_STORE: go(k_gemv_b_finish<EPI_STORE>); break;
+    case EPI_RESID: go(k_gemv_b_finish<EPI_RESID>); break;
+    case EPI_SWIGLU: go(k_gemv_b_finish<EPI_SWIGLU>); break;
+    case EPI_QKV: go(k_gemv_b_finish<EPI_QKV>); break;
+    default: go(k_gemv_b_finish<EPI_LOGITS>); break;
+    }
+    return 0;
 }
 
 // Standalone operand preparation: one thread per (vector, block of 32).

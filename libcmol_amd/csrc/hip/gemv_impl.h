@@ -9,6 +9,10 @@
 
 #include <cstdlib>
 
+// k-split finish of the batched matvec (gemv.hip): sums the `splits`
+// partial sums of every (vector, row) in a fixed order and runs the epilogue.
+int launch_gemv_b_finish(const GemvArgs &a, int epi, int splits, int ss_count, hipStream_t s);
+
 // Launch shape of one matvec (host-computed, see plan_gemv).
 struct GemvShape {
     int epi;        // GemvEpilogue
@@ -498,9 +502,214 @@ static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
     return launch_cfg<DT, 1, NG>(a, epi, s);
 }
 
+// ---------------------------------------------------------------------------
+// Batched matvec for more than 8 vectors (lock-step multi-session decode).
+//
+// The vectors are cut into groups of GB_VG = 8 (16 MFMA A rows: the high and
+// low f16 parts of each), the rows into blocks of GB_NW * tpw 16-row tiles
+// and k into `splits` ranges of sq block quads.  One work-group per (vector
+// group, row block, k range) copies that operand slice into LDS once and its
+// waves stream the weight quads of tpw contiguous tiles each, so the
+// operand is read from L2 once per work-group rather than once per tile.
+// Work-groups b, b+8, b+16, ... (one XCD) take the same row block for the
+// successive vector groups, so the weights they share stay in that XCD's L2.
+// With one k range the epilogue runs in place; otherwise the partial sums go
+// to a scratch buffer and k_gemv_b_finish adds them in a fixed order and runs
+// the epilogue.
+// ---------------------------------------------------------------------------
+#define GB_NW 4
+#define GB_VG 8
+#define GB_OP_BUDGET (64 * 1024)   // LDS bytes of one operand slice
+#define GB_TARGET_WGS 256
+
+struct GbShape {
+    int epi;
+    int groups, tpw, rblocks, splits, sq;
+    int ss_count;   // RMSNorm partials per vector (0: none)
+};
+
+static inline int gb_plan(const QTensor &w, int n, GbShape &sh)
+{
+    const int T = w.row_tiles, BQ = w.block_quads;
+    sh.groups = (n + GB_VG - 1) / GB_VG;
+    sh.splits = (BQ * 4 * 1024 + GB_OP_BUDGET - 1) / GB_OP_BUDGET;
+    sh.sq = (BQ + sh.splits - 1) / sh.splits;
+    sh.splits = (BQ + sh.sq - 1) / sh.sq;
+    for (sh.tpw = 4; sh.tpw > 1; sh.tpw >>= 1) {
+        sh.rblocks = (T + GB_NW * sh.tpw - 1) / (GB_NW * sh.tpw);
+        if (sh.groups * sh.rblocks * sh.splits >= GB_TARGET_WGS) break;
+    }
+    sh.rblocks = (T + GB_NW * sh.tpw - 1) / (GB_NW * sh.tpw);
+    // still too few work-groups: split k further
+    while (sh.groups * sh.rblocks * sh.splits < GB_TARGET_WGS && sh.sq > 1) {
+        sh.sq = (sh.sq + 1) / 2;
+        sh.splits = (BQ + sh.sq - 1) / sh.sq;
+    }
+    return sh.groups * sh.rblocks * sh.splits;
+}
+
+template <int DT, int U>
+__global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
+{
+#pragma clang fp contract(off)
+    constexpr int LB = QFmt<DT>::LANE_BYTES;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int BQ = a.w.block_quads, nblk = a.w.cols >> 5, T = a.w.row_tiles;
+    const int b = blockIdx.x;
+    const int vg = (b >> 3) % sh.groups;
+    const int rest = (b / (8 * sh.groups)) * 8 + (b & 7);
+    if (rest >= sh.rblocks * sh.splits) return;
+    const int rb = rest % sh.rblocks, ks = rest / sh.rblocks;
+    const int n = a.n, nrows = 2 * n;
+    const int v0 = vg * GB_VG, nv = min(GB_VG, n - v0);
+    const int q0 = ks * sh.sq, nq = min(sh.sq, BQ - q0);
+    const int tid = threadIdx.x, l = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t *s_op = smem;                                   // [4 sq blocks][4 groups][16 rows][16 B]
+    float *s_ss = (float *)(smem + (size_t)4 * sh.sq * 1024);   // [GB_VG][ss_count]
+    float *s_nrm = s_ss + ((GB_VG * sh.ss_count + 3) & ~3);
+
+    // ---- 1. operand slice and RMSNorm partials into LDS: lane l copies row
+    // 2*v0 + l%16 of k-group l/16 of a block (rows past the batch and blocks
+    // past the matrix re-read valid data: their products are discarded or
+    // meet zero weights) ----
+    for (int k = wid; k < 4 * nq; k += GB_NW) {
+        const int blk = min(4 * q0 + k, nblk - 1);
+        const int r = min(2 * v0 + (l & 15), nrows - 1);
+        const uint8_t *src = (const uint8_t *)a.in.q + ((((size_t)blk * 4 + (l >> 4)) * nrows) + r) * 16;
+        __builtin_amdgcn_global_load_lds((const gvoid_t *)src, (lvoid_t *)(s_op + (size_t)k * 1024), 16, 0, 0);
+    }
+    if (sh.ss_count)
+        stage_ss_dma<GB_NW>(a.in.ss + (size_t)v0 * a.in.ss_stride, a.in.ss_stride, sh.ss_count, nv, s_ss, wid, l);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. weight ring over this wave's items: quad q0+q of tile t0+j ----
+    const int t0 = (rb * GB_NW + wid) * sh.tpw;
+    const int ntw = max(0, min(sh.tpw, T - t0));
+    const int len = ntw * nq;
+    u32x4 c0[U], c1[U];
+    u32x2 dv[U];
+    uint32_t hv[U];
+    auto load_slot = [&](int u, int i) {
+        i = min(i, len - 1);
+        const int j = i / nq, q = i - j * nq;
+        const size_t cell = (size_t)(t0 + j) * BQ + q0 + q;
+        const u32x4 *p = (const u32x4 *)(a.w.qs + (cell * 64 + l) * LB);
+        c0[u] = p[0];
+        if constexpr (LB == 32) c1[u] = p[1];
+        else c1[u] = u32x4{0, 0, 0, 0};
+        dv[u] = *(const u32x2 *)(a.w.d + cell * 64 + (l & 15) * 4);
+        if constexpr (DT == DT_Q5_0) hv[u] = a.w.qh[cell * 64 + l];
+        else hv[u] = 0u;
+    };
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (u < len) load_slot(u, u);
+    }
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
+    __syncthreads();
+    // RMSNorm scale per vector of the group (wave w: vectors w, w + GB_NW)
+    if (sh.ss_count && sh.splits == 1) {
+        for (int v = wid; v < nv; v += GB_NW) {
+            float s = 0.0f;
+            for (int i = l; i < sh.ss_count; i += 64) s += s_ss[v * sh.ss_count + i];
+            s = wave_sum(s);
+            if (l == 0) s_nrm[v] = 1.0f / sqrtf(s / (float)a.w.cols + a.in.eps);
+        }
+        __syncthreads();
+    }
+
+    const int g = l >> 4, ar = l & 15;
+    const uint8_t *abase = s_op + (g * 16 + ar) * 16;
+    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc = zero4;
+    // lane l holds rows 16t + l%16 of vectors v0 + 2(l/16) + {0, 1}
+    auto finish_tile = [&](int j) {
+        const int t = t0 + j, row = t * 16 + (l & 15);
+#pragma unroll
+        for (int pr = 0; pr < 2; pr++) {
+            const int vl = 2 * (l >> 4) + pr;
+            const bool act = vl < nv && row < a.w.rows;
+            float y = (acc[2 * pr] + acc[2 * pr + 1] * LO_INV_SCALE) * ACT_INV_SCALE;
+            if (sh.splits > 1) {
+                if (act) a.part[((size_t)ks * n + v0 + vl) * a.w.rows + row] = y;
+                continue;
+            }
+            if (sh.ss_count) y *= s_nrm[vl < nv ? vl : 0];
+            const int vv = act ? v0 + vl : 0;
+            switch (sh.epi) {
+            case EPI_STORE: epilogue<EPI_STORE>(a, t, l & 15, 16, vv, act, y); break;
+            case EPI_RESID: epilogue<EPI_RESID>(a, t, l & 15, 16, vv, act, y); break;
+            case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, l & 15, 16, vv, act, y); break;
+            case EPI_QKV: epilogue<EPI_QKV>(a, t, l & 15, 16, vv, act, y); break;
+            default: epilogue<EPI_LOGITS>(a, t, l & 15, 16, vv, act, y); break;
+            }
+        }
+        acc = zero4;
+    };
+    auto compute = [&](int u, int i) {
+        const float dsc[4] = {
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] & 0xFFFFu)),
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] >> 16)),
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] & 0xFFFFu)),
+            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] >> 16))};
+        const int j = i / nq, q = i - j * nq;
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
+            const f16x8 xv = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
+            const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, zero4, 0, 0, 0);
+            acc[0] = fmaf(dsc[bi], cc[0], acc[0]);
+            acc[1] = fmaf(dsc[bi], cc[1], acc[1]);
+            acc[2] = fmaf(dsc[bi], cc[2], acc[2]);
+            acc[3] = fmaf(dsc[bi], cc[3], acc[3]);
+        }
+        if (q == nq - 1) finish_tile(j);
+    };
+    for (int i0 = 0; i0 < len; i0 += U) {
+        if (i0 + U < len) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                compute(u, i0 + u);
+                load_slot(u, i0 + u + U);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (i0 + u < len) compute(u, i0 + u);
+        }
+    }
+}
+
+template <int DT>
+static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
+{
+    if (epi < EPI_STORE || epi > EPI_LOGITS || a.w.fold != 1) return -6;
+    GbShape sh;
+    sh.epi = epi;
+    sh.ss_count = a.in.ss ? a.in.ss_count : 0;
+    const int wgs = gb_plan(a.w, a.n, sh);
+    if (sh.splits > 1 && !a.part) return -6;
+    const long blocks = (long)((sh.rblocks * sh.splits + 7) / 8) * 8 * sh.groups;
+    const size_t lds = (size_t)4 * sh.sq * 1024 + ((GB_VG * sh.ss_count + 3) & ~3) * 4 + GB_VG * 4;
+    (void)wgs;
+    constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
+    auto kern = k_gemv_b<DT, U>;
+    // kernel timing: the start event on the first kernel, the stop event on
+    // the last (the finish kernel when k is split)
+    if (a.ev_start)
+        hipExtLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GB_NW * 64), lds, s, a.ev_start,
+                              sh.splits == 1 ? a.ev_stop : nullptr, 0, a, sh);
+    else
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GB_NW * 64), lds, s, a, sh);
+    if (sh.splits > 1) return launch_gemv_b_finish(a, epi, sh.splits, sh.ss_count, s);
+    return 0;
+}
+
 template <int DT>
 int launch_ng(const GemvArgs &a, int epi, hipStream_t s)
 {
+    if (a.n > GB_VG && a.w.fold == 1) return launch_gemv_b<DT>(a, epi, s);
     const int rows = 2 * a.n * a.w.fold;   // MFMA A rows
     if (rows <= 16) return launch_dt<DT, 1>(a, epi, s);
     if (rows <= 32) return launch_dt<DT, 2>(a, epi, s);

@@ -137,9 +137,15 @@ struct GemvArgs {
     unsigned long long *argmax;   // ARGMAX_SLOTS slots per vector
     // when set, recorded at the kernel's own start and end (kernel timing)
     hipEvent_t ev_start, ev_stop;
+    // batches of more than 8 vectors: k-split partial sums, at least
+    // gemv_part_floats(w, n) floats (unused when that is 0)
+    float *part;
 };
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);
+// Scratch floats a batched (n > 8) matvec over w needs for its k-split
+// partial sums (0 when it does not split k).
+size_t gemv_part_floats(const QTensor &w, int n);
 // The same product for many vectors (prompt tokens): 64 x 64 output tiles,
 // epilogues EPI_STORE..EPI_QKV; any n >= 1.
 int launch_gemm(const GemvArgs &a, int epi, hipStream_t s);

@@ -131,6 +131,36 @@ def test_gemm_tiled_rmsnorm_prologue(ctx):
     assert_close(got, want, "tiled gemm with rmsnorm")
 
 
+@pytest.mark.parametrize("dtype,rows,cols,n", [
+    (2, 3072, 2048, 32), (2, 2048, 11008, 32), (2, 22016, 2048, 32), (6, 960, 2560, 16),
+    (8, 576, 576, 24), (2, 300, 2048, 9), (6, 1600, 960, 16), (8, 4104, 576, 12)])
+def test_gemv_batched_groups_match_oracle(ctx, dtype, rows, cols, n):
+    """9..32 vectors: vector groups of 8, operand slices staged once per
+    work-group, k splits summed by the finish kernel; partial row tiles and
+    partial vector groups included."""
+    raw = random_blocks(dtype, rows, cols, seed=rows + 7 * cols + n)
+    x = np.random.default_rng(n + 3).standard_normal((n, cols)).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.gemm(t, x)
+    want = O.matmul(raw, np.ascontiguousarray(x.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"batched gemv q{dtype} {rows}x{cols} n {n}")
+
+
+def test_gemv_batched_groups_rmsnorm(ctx):
+    """The batched path applies each vector's RMSNorm scale (in place and in
+    the k-split finish)."""
+    rng = np.random.default_rng(17)
+    for rows, cols, n in ((512, 2048, 20), (256, 11008, 16)):
+        raw = random_blocks(2, rows, cols, seed=rows + n)
+        x = (rng.standard_normal((n, cols)) * 2).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+        t = ctx.qtensor([raw], 2, cols, [rows])
+        got = ctx.gemm(t, x, norm_w=w, eps=1e-6)
+        xn = np.stack([O.rms_norm(xi, w, 1e-6) for xi in x])
+        want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, 2, O.AVX512).T
+        assert_close(got, want, f"batched gemv rmsnorm {rows}x{cols} n {n}")
+
+
 def test_gemv_rmsnorm_prologue(ctx):
     rows, cols, dtype = 256, 2048, 2
     raw = random_blocks(dtype, rows, cols, seed=9)
