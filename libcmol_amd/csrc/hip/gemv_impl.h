@@ -517,7 +517,7 @@ static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
 // to a scratch buffer and k_gemv_b_finish adds them in a fixed order and runs
 // the epilogue.
 // ---------------------------------------------------------------------------
-#define GB_NW 4
+#define GB_NW 8
 #define GB_VG 8
 #define GB_OP_BUDGET (64 * 1024)   // LDS bytes of one operand slice
 #define GB_TARGET_WGS 256
