@@ -19,6 +19,201 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
     attn_merge_head<DH, ATT_THREADS, StPlain>(a, blockIdx.x, blockIdx.y);
 }
 
+// Head-per-wave decode attention for d_head 64 and 128: one work-group of
+// four waves per (kv head, split, vector); wave w serves query heads w and
+// w + 4 of the group.  The split is walked in chunks of 64 positions whose
+// K and V rows are staged in LDS by all 256 threads (coalesced 16-byte
+// loads of the next chunk are in flight while the current one is used):
+//   * scores: four lanes per position, each holding a quarter of the head's
+//     query in registers (interleaved 16-byte pieces) against the same pieces
+//     of the K row; K rows are padded to an odd multiple of 64 bytes so the
+//     four rows a 16-lane pass reads fall in alternate LDS bank halves;
+//   * online softmax over the 64 scores with wave reductions;
+//   * weighted sum with lanes over the dimensions: each position's weight is
+//     broadcast with readlane and its V row read once per wave.
+// Same partial format as attn_split, merged by k_attn_merge.
+#define ATH_CH 64
+template <int DH, typename KT>
+__global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
+{
+#pragma clang fp contract(off)
+    constexpr int RB = DH * (int)sizeof(KT);        // row bytes
+    constexpr int KS = RB + 64;                      // padded K row stride (bytes)
+    constexpr int PE = 16 / (int)sizeof(KT);         // elements per 16-byte piece
+    constexpr int NPL = RB / 16 / 4;                 // pieces per lane (a quarter of the row)
+    constexpr int DL = DH / 64;                      // output dims per lane
+    constexpr int UNITS = ATH_CH * RB / 16;          // 16-byte units of a chunk's K (and of V)
+    constexpr int UPT = UNITS / 256;                 // per thread
+    static_assert(UNITS % 256 == 0, "chunk size");
+    __shared__ __attribute__((aligned(16))) uint8_t ks[2][ATH_CH * KS];
+    __shared__ __attribute__((aligned(16))) uint8_t vs[2][ATH_CH * RB];
+
+    const int kvh = blockIdx.x, sp = blockIdx.y, n = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.n_heads / a.n_kv;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int t0 = sp * a.split;
+    if (t0 >= L) return;
+    const int cnt = min(L, t0 + a.split) - t0;
+    const int nch = (cnt + ATH_CH - 1) / ATH_CH;
+    const int nact = (L + a.split - 1) / a.split;
+    const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
+    const uint8_t *kb = (const uint8_t *)((const KT *)a.kv.k_base + off);
+    const uint8_t *vb = (const uint8_t *)((const KT *)a.kv.v_base + off);
+
+    // staging: thread tid moves units tid + 256u of K and V (rows past the
+    // split re-read its last row; their weights are zero)
+    u32x4 kr[UPT], vr[UPT];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const int unit = tid + 256 * u, row = unit / (RB / 16), col = unit % (RB / 16);
+            const size_t src = (size_t)min(c * ATH_CH + row, cnt - 1) * RB + col * 16;
+            kr[u] = ldg((const u32x4 *)(kb + src));
+            vr[u] = ldg((const u32x4 *)(vb + src));
+        }
+    };
+    auto put = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const int unit = tid + 256 * u, row = unit / (RB / 16), col = unit % (RB / 16);
+            *(u32x4 *)&ks[buf][row * KS + col * 16] = kr[u];
+            *(u32x4 *)&vs[buf][row * RB + col * 16] = vr[u];
+        }
+    };
+
+    // queries of this wave's heads: lane quarter j holds pieces j, j+4, ...
+    const int j = lane & 3;
+    const int nh = wid < G ? (wid + 4 < G ? 2 : 1) : 0;
+    float q[2][NPL * PE];
+    float m[2], l[2], o[2][DL];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        m[hh] = -INFINITY;
+        l[hh] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DL; d++) o[hh][d] = 0.0f;
+        const int g = min(wid + 4 * hh, G - 1);
+        const float *qh = a.q + (size_t)n * a.q_stride + (size_t)(kvh * G + g) * DH;
+#pragma unroll
+        for (int i = 0; i < NPL; i++)
+#pragma unroll
+            for (int e = 0; e < PE; e++) q[hh][i * PE + e] = ldg(qh + (j + 4 * i) * PE + e);
+    }
+    const float scale = 1.0f / sqrtf((float)DH);
+
+    fetch(0);
+    put(0);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        if (c + 1 < nch) fetch(c + 1);
+        const int np = min(ATH_CH, cnt - c * ATH_CH);
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            if (hh >= nh) break;
+            // scores: pass ps covers positions 16 ps + lane/4
+            float sc[4];
+#pragma unroll
+            for (int ps = 0; ps < 4; ps++) {
+                const uint8_t *kr0 = &ks[buf][(16 * ps + (lane >> 2)) * KS];
+                float dot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NPL; i++) {
+                    const u32x4 w = *(const u32x4 *)(kr0 + (j + 4 * i) * 16);
+                    float kv[PE];
+                    if constexpr (sizeof(KT) == 4) {
+                        const f32x4 wf = __builtin_bit_cast(f32x4, w);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) kv[e] = wf[e];
+                    } else {
+                        const f16x8 h8 = __builtin_bit_cast(f16x8, w);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) kv[e] = (float)h8[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < PE; e++) dot = fmaf(q[hh][i * PE + e], kv[e], dot);
+                }
+                dot += __shfl_xor(dot, 1, 64);
+                dot += __shfl_xor(dot, 2, 64);
+                sc[ps] = (16 * ps + (lane >> 2)) < np ? dot * scale : -INFINITY;
+            }
+            float mc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            mc = wave_max(mc);
+            const float mn = fmaxf(m[hh], mc);
+            float ev[4], ls = 0.0f;
+#pragma unroll
+            for (int ps = 0; ps < 4; ps++) {
+                ev[ps] = expf(sc[ps] - mn);
+                if (j == 0) ls += ev[ps];
+            }
+            ls = wave_sum(ls);
+            const float al = expf(m[hh] - mn);
+            l[hh] = l[hh] * al + ls;
+            m[hh] = mn;
+#pragma unroll
+            for (int d = 0; d < DL; d++) o[hh][d] *= al;
+            // weighted sum: lane covers dims DL*lane ..
+#pragma unroll
+            for (int ps = 0; ps < 4; ps++) {
+#pragma unroll 4
+                for (int r = 0; r < 16; r++) {
+                    const float ep = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[ps]), 4 * r));
+                    const uint8_t *vrow = &vs[buf][(16 * ps + r) * RB];
+                    if constexpr (sizeof(KT) == 4) {
+                        if constexpr (DL == 2) {
+                            const float2 v = *(const float2 *)(vrow + lane * 8);
+                            o[hh][0] = fmaf(ep, v.x, o[hh][0]);
+                            o[hh][1] = fmaf(ep, v.y, o[hh][1]);
+                        } else {
+                            o[hh][0] = fmaf(ep, *(const float *)(vrow + lane * 4), o[hh][0]);
+                        }
+                    } else {
+                        if constexpr (DL == 2) {
+                            const f16x2 v = *(const f16x2 *)(vrow + lane * 4);
+                            o[hh][0] = fmaf(ep, (float)v[0], o[hh][0]);
+                            o[hh][1] = fmaf(ep, (float)v[1], o[hh][1]);
+                        } else {
+                            o[hh][0] = fmaf(ep, (float)*(const _Float16 *)(vrow + lane * 2), o[hh][0]);
+                        }
+                    }
+                }
+            }
+        }
+        if (c + 1 < nch) {
+            __syncthreads();   // every wave is done with the other buffer
+            put(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // partials (or the finished output when the session fits one split)
+    const bool single = nact == 1;
+    const size_t sbase = (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        if (hh >= nh) break;
+        const int g = wid + 4 * hh;
+#pragma unroll
+        for (int d = 0; d < DL; d++) {
+            const int dim = DL * lane + d;
+            if (single) {
+                const float ov = o[hh][d] / l[hh];
+                const int k = (kvh * G + g) * DH + dim;
+                if (a.out) a.out[(size_t)n * a.out_stride + k] = ov;
+                if (a.next.q) act_put(a.next, n, k, ov);
+            } else {
+                a.po[(sbase + g) * DH + dim] = o[hh][d];
+            }
+        }
+        if (!single && lane == 0) {
+            a.pm[sbase + g] = m[hh];
+            a.pl[sbase + g] = l[hh];
+        }
+    }
+}
+
 int attn_max_splits(int max_ctx, int split) { return (max_ctx + split - 1) / split; }
 
 int launch_attn(const AttnArgs &a, hipStream_t s)
@@ -30,16 +225,32 @@ int launch_attn(const AttnArgs &a, hipStream_t s)
     dim3 grid(a.n_kv, a.max_splits, a.n), block(ATT_THREADS), mgrid(a.n_heads, a.n);
 #define ATT(DHV)                                                                          \
     if (a.kv_f16) hipLaunchKernelGGL((k_attn<DHV, _Float16>), grid, block, 0, s, a);      \
-    else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);                  \
-    if (a.max_splits > 1) hipLaunchKernelGGL((k_attn_merge<DHV>), mgrid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);
+#define ATH(DHV)                                                                          \
+    if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16>), grid, block, 0, s, a);    \
+    else hipLaunchKernelGGL((k_attn_h<DHV, float>), grid, block, 0, s, a);
+    // head-per-wave kernel for short splits (one or two chunks); the
+    // thread-per-dimension kernel streams long splits better
+    const char *e = getenv("CMOL_ATTN_H");
+    const bool head_waves = e ? e[0] == '1' : a.split <= 2 * ATH_CH;
     switch (a.d_head) {
     case 16: ATT(16); break;
     case 32: ATT(32); break;
-    case 64: ATT(64); break;
-    case 128: ATT(128); break;
+    case 64: if (head_waves) { ATH(64); } else { ATT(64); } break;
+    case 128: if (head_waves) { ATH(128); } else { ATT(128); } break;
     case 256: ATT(256); break;
     default: return -4;
     }
+    if (a.max_splits > 1) {
+        switch (a.d_head) {
+        case 16: hipLaunchKernelGGL((k_attn_merge<16>), mgrid, block, 0, s, a); break;
+        case 32: hipLaunchKernelGGL((k_attn_merge<32>), mgrid, block, 0, s, a); break;
+        case 64: hipLaunchKernelGGL((k_attn_merge<64>), mgrid, block, 0, s, a); break;
+        case 128: hipLaunchKernelGGL((k_attn_merge<128>), mgrid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_attn_merge<256>), mgrid, block, 0, s, a); break;
+        }
+    }
 #undef ATT
+#undef ATH
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
