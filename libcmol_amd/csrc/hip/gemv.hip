@@ -67,7 +67,7 @@ int launch_gemm(const GemvArgs &a, int epi, hipStream_t s)
 
 size_t gemv_part_floats(const QTensor &w, int n)
 {
-    if (n <= GB_VG || w.fold != 1) return 0;
+    if (!gemv_batched(w, n)) return 0;
     GbShape sh;
     gb_plan(w, n, sh);
     return sh.splits > 1 ? (size_t)sh.splits * n * w.rows : 0;

@@ -136,10 +136,10 @@ __device__ __forceinline__ float2 rope_cs(const GemvArgs &a, int row, int pos)
 // (roped) and v rows -> the KV cache at pos; `partner` is the pair's other
 // row (row ^ 1).
 template <typename M>
-__device__ __forceinline__ void qkv_out(const GemvArgs &a, int v, int row, float y, float partner, float2 cs, int pos)
+__device__ __forceinline__ void qkv_out(const GemvArgs &a, int v, int row, float y, float partner, float2 cs, int pos,
+                                        size_t kvo)
 {
 #pragma clang fp contract(off)
-    const size_t kvo = kv_offset(a.kv, v);
     if (row < a.nq + a.nkv) {
         const int rr = row < a.nq ? row : row - a.nq;
         const int i = rr % a.d_head;
@@ -161,11 +161,61 @@ __device__ __forceinline__ void qkv_out(const GemvArgs &a, int v, int row, float
     }
 }
 
+// Epilogue inputs a matvec loads at its start, while its weights stream in,
+// so that the epilogue does not wait on memory: the residual (EPI_RESID);
+// the position, cache offset and RoPE (cos, sin) of the row (EPI_QKV).
+struct EpiPre {
+    float x = 0.0f;
+    int pos = 0, slot = 0;
+    size_t kvo = 0;
+    float2 cs = {1.0f, 0.0f};
+};
+
+// First part, for output (vector v, row): three unconditional loads (a
+// load whose value the epilogue does not need reads the operand buffer
+// instead), so that no branch and no use of a loaded value makes the
+// kernel wait here; epi_pre_cs interprets them.
+__device__ __forceinline__ void epi_pre_load(const GemvArgs &a, int epi, int v, int row, bool act, EpiPre &p)
+{
+    const float *dummy = (const float *)a.in.q;
+    const bool resid = act && epi == EPI_RESID, qkv = act && epi == EPI_QKV;
+    const float *xa = resid ? (a.res ? a.res : a.out) + ((size_t)v * a.out_stride + row) : dummy;
+    const int *pa = qkv && a.pos ? a.pos + (size_t)v * a.pos_stride : (const int *)dummy;
+    const int *sa = qkv && a.kv.slot_ids ? a.kv.slot_ids + v : (const int *)dummy;
+    p.x = *gptr(xa);
+    p.pos = *gptr(pa);
+    p.slot = *gptr(sa);
+}
+
+// Second part, once the first part's loads have landed: the clamped
+// position, the cache offset, and the RoPE pair of the row.
+__device__ __forceinline__ void epi_pre_cs(const GemvArgs &a, int epi, int row, bool act, EpiPre &p)
+{
+    if (act && epi == EPI_QKV) {
+        const int pos = a.pos ? p.pos : a.pos0;
+        p.pos = min(max(pos, 0), a.max_ctx - 1);
+        p.kvo = (a.kv.slot_ids ? (size_t)p.slot * a.kv.slot_stride : 0) + a.kv.layer_off;
+        p.cs = rope_cs(a, row, p.pos);
+    }
+}
+
+// Pins a launch argument in SGPRs at this point: the kernel-argument loads
+// of every pinned value are then issued together and waited for once,
+// instead of being sunk into the branches that first use them (each sunk
+// group is another round trip before the weight loads go out).
+template <typename T>
+__device__ __forceinline__ void sgpr_pin(T v)
+{
+    asm volatile("" ::"s"(v));
+}
+
 // Epilogue for vector v, weight row R*t + rl.  Every lane of the wave calls
 // it (shuffles within aligned groups of R lanes, one group per (vector,
-// tile)); `act` marks lanes whose (row, v) is real.
+// tile)); `act` marks lanes whose (row, v) is real.  With `has_pre`, `pre`
+// holds this output's inputs loaded by epi_pre_load / epi_pre_cs.
 template <int EPI, typename M = StPlain>
-__device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R, int v, bool act, float y)
+__device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R, int v, bool act, float y,
+                                         bool has_pre = false, EpiPre pre = EpiPre())
 {
 #pragma clang fp contract(off)
     const int row = t * R + rl;
@@ -176,7 +226,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
         float x = 0.0f;
         if (act) {
             const size_t i = (size_t)v * a.out_stride + row;
-            x = (a.res ? a.res[i] : a.out[i]) + y;
+            x = (has_pre ? pre.x : a.res ? a.res[i] : a.out[i]) + y;
         }
         resid_out<M>(a, t, rl, R, v, act, x);
     } else if constexpr (EPI == EPI_SWIGLU) {
@@ -189,8 +239,12 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
     } else if constexpr (EPI == EPI_QKV) {
         const float partner = __shfl_xor(y, 1, 64);
         if (act) {
-            const int pos = epi_pos(a, v);
-            qkv_out<M>(a, v, row, y, partner, rope_cs(a, row, pos), pos);
+            if (has_pre) {
+                qkv_out<M>(a, v, row, y, partner, pre.cs, pre.pos, pre.kvo);
+            } else {
+                const int pos = epi_pos(a, v);
+                qkv_out<M>(a, v, row, y, partner, rope_cs(a, row, pos), pos, kv_offset(a.kv, v));
+            }
         }
     } else if constexpr (EPI == EPI_LOGITS) {
         if (act) a.out[(size_t)v * a.out_stride + row] = y;
@@ -216,16 +270,46 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
 // part c / R, so only the entries with matching parts are used.  Each wave
 // combines its high/low pairs and leaves the useful entries in LDS, where one
 // thread per (vector, row) sums them over waves and parts in a fixed order.
-template <int DT, int NW, int NG, bool CHUNKED, int U>
+//
+// EPI >= 0 fixes the epilogue at compile time (the decode kernels: one
+// straight code path, so that a launch's cold instruction cache fetches
+// little); EPI < 0 takes it from sh.epi.
+template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI>
 __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
 {
     constexpr int LB = QFmt<DT>::LANE_BYTES;
+    // launch arguments needed before the weight loads go out, fetched in
+    // one round trip
+    sgpr_pin(a.w.qs);
+    sgpr_pin(a.w.d);
+    if constexpr (DT == DT_Q5_0) sgpr_pin(a.w.qh);
+    sgpr_pin(a.w.rows);
+    sgpr_pin(a.w.cols);
+    sgpr_pin(a.w.block_quads);
+    sgpr_pin(a.w.fold);
+    sgpr_pin(a.n);
+    sgpr_pin(a.in.q);
+    sgpr_pin(a.in.ss);
+    sgpr_pin(a.in.ss_count);
+    sgpr_pin(a.in.ss_stride);
+    sgpr_pin(sh.qpc);
+    sgpr_pin(sh.zslot);
+    sgpr_pin(sh.epi);
+    sgpr_pin(a.out);
+    sgpr_pin(a.res);
+    sgpr_pin(a.out_stride);
+    sgpr_pin(a.pos);
+    sgpr_pin(a.pos_stride);
+    sgpr_pin(a.kv.slot_ids);
+    const int epi = EPI >= 0 ? EPI : sh.epi;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *s_op = smem;
     float *s_ss = (float *)(smem + sh.op_bytes);
     float *s_nrm = (float *)(smem + sh.op_bytes + sh.ss_bytes);
+    float *s_z = s_nrm + ((a.n + 3) & ~3);
 
-    const int BQ = a.w.block_quads, F = a.w.fold, R = 16 / F;
+    // fold F = 2^lf (1..8) parts of R = 16/F = 2^lr rows per tile
+    const int BQ = a.w.block_quads, F = a.w.fold, lf = __builtin_ctz(F), lr = 4 - lf, R = 1 << lr;
     const int t = blockIdx.x;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
     const int n = a.n;
@@ -235,6 +319,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     const int nchunks = CHUNKED ? (BQ + cq - 1) / cq : 1;
     const int len = nchunks * qpc;
     const size_t cell0 = (size_t)t * BQ;
+
+    // ---- 0. the epilogue inputs, when every output of the tile has a
+    // thread of its own (one pass of step 6) ----
+    const bool pre_on = n * R <= NW * 64;
+    const int pv = (int)threadIdx.x >> lr, prow = t * R + ((int)threadIdx.x & (R - 1));
+    const bool pact = pre_on && (int)threadIdx.x < n * R && prow < a.w.rows;
+    EpiPre pre;
+    epi_pre_load(a, epi, pv, prow, pact, pre);
 
     // ---- 1. operand and norm partials into LDS (issued first) ----
     if constexpr (!CHUNKED) stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
@@ -275,6 +367,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(LPS * U));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    epi_pre_cs(a, epi, prow, pact, pre);
 
     // A-operand row fed by this lane per group: LDS address of block 0 and
     // per-block stride (rows beyond 2nF read the zero slot)
@@ -283,7 +376,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
 #pragma unroll
     for (int gi = 0; gi < NG; gi++) {
         const int ar = 16 * gi + (l & 15);
-        const int v = ar / (2 * F), p = (ar >> 1) % F, h = ar & 1;
+        const int v = ar >> (lf + 1), p = (ar >> 1) & (F - 1), h = ar & 1;
         const bool ok = v < n;
         const int p0 = CHUNKED ? 0 : p * 4 * BQ;
         abase[gi] = ok ? p0 * vb + (g * 2 * n + 2 * v + h) * 16 : sh.zslot;
@@ -307,6 +400,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
         }
         const int lq = wid * qpc + j;
         if (c * cq + lq >= BQ) return;
+        // the quad's four operand reads go out together, ahead of the decode
+        f16x8 xv[4][NG];
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++)
+                xv[bi][gi] = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
+        }
         const float dsc[4] = {
             (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] & 0xFFFFu)),
             (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] >> 16)),
@@ -317,8 +418,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
             const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
 #pragma unroll
             for (int gi = 0; gi < NG; gi++) {
-                const f16x8 xv = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
-                const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, zero4, 0, 0, 0);
+                const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[bi][gi], wv, zero4, 0, 0, 0);
                 acc[gi][0] = fmaf(dsc[bi], cc[0], acc[gi][0]);
                 acc[gi][1] = fmaf(dsc[bi], cc[1], acc[gi][1]);
                 acc[gi][2] = fmaf(dsc[bi], cc[2], acc[gi][2]);
@@ -343,7 +443,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     }
 
     // ---- 4. RMSNorm scale per vector from the staged partials ----
-    if (a.in.ss) {
+    if (EPI != EPI_RESID && a.in.ss) {
         for (int v = wid; v < n; v += NW) {
             float s = 0.0f;
             for (int i = l; i < a.in.ss_count; i += 64) s += s_ss[v * a.in.ss_count + i];
@@ -354,17 +454,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     // ---- 5. the waves' useful entries meet in LDS: lane l (column c = part
     // p x row rl) holds, per group and component pair, the high/low parts of
     // A row 2(vF + p') + h; the pairs with p' == p are combined and stored at
-    // s_z[w][v][rl][p] ----
-    __syncthreads();   // every wave is done with the operand area
-    float *s_z = (float *)smem;
+    // s_z[w][v][rl][p], an LDS area of its own (no wait for the other waves
+    // to finish with the operand) ----
     {
-        const int c = l & 15, pc = c / R, rc = c % R;
+        const int c = l & 15, pc = c >> lr, rc = c & (R - 1);
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
 #pragma unroll
             for (int q = 0; q < 2; q++) {
                 const int ar = 16 * gi + 4 * (l >> 4) + 2 * q;
-                const int v = ar / (2 * F), pp = (ar >> 1) % F;
+                const int v = ar >> (lf + 1), pp = (ar >> 1) & (F - 1);
                 if (v < n && pp == pc)
                     s_z[((wid * n + v) * R + rc) * F + pp] = acc[gi][2 * q] + acc[gi][2 * q + 1] * LO_INV_SCALE;
             }
@@ -378,7 +477,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     for (int o0 = 0; o0 < nout; o0 += NW * 64) {
         const int o = o0 + (int)threadIdx.x;
         const bool act = o < nout;
-        const int v = act ? o / R : 0, rl = o % R;
+        const int v = act ? o >> lr : 0, rl = o & (R - 1);
         float z = 0.0f;
         if (act) {
             const float *zp = s_z + ((size_t)v * R + rl) * F;
@@ -407,13 +506,17 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
             }
         }
         float y = z * ACT_INV_SCALE;
-        if (a.in.ss) y *= s_nrm[v];
-        switch (sh.epi) {
-        case EPI_STORE: epilogue<EPI_STORE>(a, t, rl, R, v, act, y); break;
-        case EPI_RESID: epilogue<EPI_RESID>(a, t, rl, R, v, act, y); break;
-        case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, rl, R, v, act, y); break;
-        case EPI_QKV: epilogue<EPI_QKV>(a, t, rl, R, v, act, y); break;
-        default: epilogue<EPI_LOGITS>(a, t, rl, R, v, act, y); break;
+        if (EPI != EPI_RESID && a.in.ss) y *= s_nrm[v];
+        if constexpr (EPI >= 0) {
+            epilogue<EPI >= 0 ? EPI : 0>(a, t, rl, R, v, act, y, pre_on, pre);
+        } else {
+            switch (sh.epi) {
+            case EPI_STORE: epilogue<EPI_STORE>(a, t, rl, R, v, act, y); break;
+            case EPI_RESID: epilogue<EPI_RESID>(a, t, rl, R, v, act, y, pre_on, pre); break;
+            case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, rl, R, v, act, y); break;
+            case EPI_QKV: epilogue<EPI_QKV>(a, t, rl, R, v, act, y, pre_on, pre); break;
+            default: epilogue<EPI_LOGITS>(a, t, rl, R, v, act, y); break;
+            }
         }
     }
 }
@@ -441,7 +544,7 @@ static inline int plan_gemv(const GemvArgs &a, int nw, GemvShape &sh, bool &chun
     sh.ss_bytes = a.in.ss ? round_up(a.n * a.in.ss_count * 4, 16) : 0;
     const int nrm = round_up(a.n * 4, 16);
     const int red = nw * a.n * 64;   // per-wave useful entries (16 columns x n floats)
-    const int cap = GEMV_LDS_BUDGET - sh.ss_bytes - nrm - 16;
+    const int cap = GEMV_LDS_BUDGET - sh.ss_bytes - nrm - red - 16;
     const long full = (long)F * 4 * BQ * vb;
     if (full <= cap) {
         chunked = false;
@@ -454,9 +557,54 @@ static inline int plan_gemv(const GemvArgs &a, int nw, GemvShape &sh, bool &chun
         if (sh.qpc < 1) return -1;
         sh.zslot = 4 * sh.qpc * nw * vb;
     }
-    sh.op_bytes = round_up(sh.zslot + 16 > red ? sh.zslot + 16 : red, 16);
-    return sh.op_bytes + sh.ss_bytes + nrm;
+    sh.op_bytes = round_up(sh.zslot + 16, 16);
+    return sh.op_bytes + sh.ss_bytes + nrm + red;
 }
+
+// Ring depths: the long ring, and the short one for a wave whose whole run
+// fits it.
+template <int DT>
+struct GemvRing {
+    static constexpr int L = DT == DT_Q8_0 ? 6 : 8, S = L / 2;
+};
+
+template <typename K>
+static void gemv_go(K kern, const GemvArgs &a, const GemvShape &sh, int lds, int nw, hipStream_t s)
+{
+    const dim3 grid(a.w.row_tiles), block(nw * 64);
+    if (a.ev_start) hipExtLaunchKernelGGL(kern, grid, block, lds, s, a.ev_start, a.ev_stop, 0, a, sh);
+    else hipLaunchKernelGGL(kern, grid, block, lds, s, a, sh);
+}
+
+// Launch of the one-group kernel with its epilogue fixed at compile time
+// (instantiated per format in gemv_q*_epi.hip).
+template <int DT, int NW>
+int launch_gemv_epi(const GemvArgs &a, const GemvShape &sh, int lds, int len, hipStream_t s);
+
+#ifdef GEMV_EPI_TU
+template <int DT, int NW, int EPI>
+static void launch_epi_u(const GemvArgs &a, const GemvShape &sh, int lds, int len, hipStream_t s)
+{
+    using RG = GemvRing<DT>;
+    if (len <= 2) gemv_go(k_gemv<DT, NW, 1, false, 2, EPI>, a, sh, lds, NW, s);
+    else if (len <= RG::S) gemv_go(k_gemv<DT, NW, 1, false, RG::S, EPI>, a, sh, lds, NW, s);
+    else gemv_go(k_gemv<DT, NW, 1, false, RG::L, EPI>, a, sh, lds, NW, s);
+}
+
+template <int DT, int NW>
+int launch_gemv_epi(const GemvArgs &a, const GemvShape &sh, int lds, int len, hipStream_t s)
+{
+    switch (sh.epi) {
+    case EPI_STORE: launch_epi_u<DT, NW, EPI_STORE>(a, sh, lds, len, s); break;
+    case EPI_RESID: launch_epi_u<DT, NW, EPI_RESID>(a, sh, lds, len, s); break;
+    case EPI_SWIGLU: launch_epi_u<DT, NW, EPI_SWIGLU>(a, sh, lds, len, s); break;
+    case EPI_QKV: launch_epi_u<DT, NW, EPI_QKV>(a, sh, lds, len, s); break;
+    case EPI_LOGITS: launch_epi_u<DT, NW, EPI_LOGITS>(a, sh, lds, len, s); break;
+    default: return -6;
+    }
+    return 0;
+}
+#endif
 
 template <int DT, int NW, int NG>
 static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
@@ -467,20 +615,19 @@ static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
     bool chunked = false;
     const int lds = plan_gemv(a, NW, sh, chunked);
     if (lds < 0) return -6;
-    const dim3 grid(a.w.row_tiles), block(NW * 64);
-    // ring depth: the short ring when a wave's whole run fits it
-    constexpr int UL = (DT == DT_Q8_0) ? 6 : 8, US = UL / 2;
+    using RG = GemvRing<DT>;
     const int len = chunked ? ((a.w.block_quads + sh.qpc * NW - 1) / (sh.qpc * NW)) * sh.qpc : sh.qpc;
-    auto go = [&](auto kern) {
-        if (a.ev_start) hipExtLaunchKernelGGL(kern, grid, block, lds, s, a.ev_start, a.ev_stop, 0, a, sh);
-        else hipLaunchKernelGGL(kern, grid, block, lds, s, a, sh);
-    };
+    // the decode shape (one operand group, operand staged whole; residual
+    // epilogues take no RMSNorm there) runs the epilogue-specialised kernel
+    if constexpr (NG == 1) {
+        if (!chunked && !(epi == EPI_RESID && a.in.ss)) return launch_gemv_epi<DT, NW>(a, sh, lds, len, s);
+    }
     if (chunked) {
-        if (len <= US) go(k_gemv<DT, NW, NG, true, US>);
-        else go(k_gemv<DT, NW, NG, true, UL>);
+        if (len <= RG::S) gemv_go(k_gemv<DT, NW, NG, true, RG::S, -1>, a, sh, lds, NW, s);
+        else gemv_go(k_gemv<DT, NW, NG, true, RG::L, -1>, a, sh, lds, NW, s);
     } else {
-        if (len <= US) go(k_gemv<DT, NW, NG, false, US>);
-        else go(k_gemv<DT, NW, NG, false, UL>);
+        if (len <= RG::S) gemv_go(k_gemv<DT, NW, NG, false, RG::S, -1>, a, sh, lds, NW, s);
+        else gemv_go(k_gemv<DT, NW, NG, false, RG::L, -1>, a, sh, lds, NW, s);
     }
     return 0;
 }
@@ -495,7 +642,11 @@ static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
         bool ch;
         if (nw <= 1 || plan_gemv(a, nw, sh, ch) >= 0) break;
     }
-    if (nw >= 16) return launch_cfg<DT, 16, NG>(a, epi, s);
+    // 16 waves leave 128 VGPRs a lane: only the single-group Q4_0 kernel
+    // fits without spilling
+    if constexpr (NG == 1 && DT == DT_Q4_0) {
+        if (nw >= 16) return launch_cfg<DT, 16, NG>(a, epi, s);
+    }
     if (nw >= 8) return launch_cfg<DT, 8, NG>(a, epi, s);
     if (nw >= 4) return launch_cfg<DT, 4, NG>(a, epi, s);
     if (nw >= 2) return launch_cfg<DT, 2, NG>(a, epi, s);
@@ -521,6 +672,17 @@ static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
 #define GB_VG 8
 #define GB_OP_BUDGET (64 * 1024)   // LDS bytes of one operand slice
 #define GB_TARGET_WGS 256
+
+// Whether a matvec of n vectors over w runs the batched kernel rather than
+// k_gemv.  CMOL_GEMV_B=1 in the environment sends every unfolded matrix there.
+static inline bool gemv_batched(const QTensor &w, int n)
+{
+    static const bool forced = [] {
+        const char *e = getenv("CMOL_GEMV_B");
+        return e && e[0] == '1';
+    }();
+    return w.fold == 1 && (n > GB_VG || forced);
+}
 
 struct GbShape {
     int epi;
@@ -709,7 +871,7 @@ static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
 template <int DT>
 int launch_ng(const GemvArgs &a, int epi, hipStream_t s)
 {
-    if (a.n > GB_VG && a.w.fold == 1) return launch_gemv_b<DT>(a, epi, s);
+    if (gemv_batched(a.w, a.n)) return launch_gemv_b<DT>(a, epi, s);
     const int rows = 2 * a.n * a.w.fold;   // MFMA A rows
     if (rows <= 16) return launch_dt<DT, 1>(a, epi, s);
     if (rows <= 32) return launch_dt<DT, 2>(a, epi, s);

@@ -304,7 +304,8 @@ __device__ __forceinline__ void pk_gemv(const GemvArgs &a, const float *xin, con
             resid_out<StDev>(a, t, l, R, 0, act, x);
         } else if constexpr (EPI == EPI_QKV) {
             const float partner = __shfl_xor(y, 1, 64);
-            if (act) qkv_out<StDev>(a, 0, row, y, partner, kt == 0 ? pcs : rope_cs(a, row, a.pos0), a.pos0);
+            if (act) qkv_out<StDev>(a, 0, row, y, partner, kt == 0 ? pcs : rope_cs(a, row, a.pos0), a.pos0,
+                                    kv_offset(a.kv, 0));
         } else {
             epilogue<EPI, StDev>(a, t, l, R, 0, l < R, y);
         }
