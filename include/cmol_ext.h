@@ -47,6 +47,23 @@ int cmol__decode_batch(cmol_session_t *const *ss, const int32_t *tokens, int n,
  * seeded synthetic values and set its length to n_tokens. */
 int cmol__session_fill_kv(cmol_session_t *s, int n_tokens, uint64_t seed);
 
+/* The host sampler, exported for parity checks; same signatures and
+ * semantics as the reference's (src/sampler.h:20-34, src/sampler.c:171-268):
+ * cmol_sample scales, softmaxes and may reorder `logits` in place;
+ * rng_state is a 4-word xoshiro256** state seeded by cmol_rng_seed. */
+int32_t cmol_sample(float *logits, int vocab_size, const cmol_gen_params_t *params,
+                    uint64_t *rng_state);
+void cmol_rng_seed(uint64_t state[4], unsigned int seed);
+uint64_t cmol_rng_next(uint64_t state[4]);
+void cmol_apply_repeat_penalty(float *logits, int vocab_size, const int32_t *tokens,
+                               int n_tokens, float penalty);
+
+/* Parse a GGUF and build its tokenizer only, without a device or sessions:
+ * cmol_encode, cmol_decode_token and cmol_free work on the result (text-path
+ * parity checks on machines without a GPU).  Same errors as cmol_load's
+ * parse stage. */
+cmol_model_t *cmol__load_text(const char *path, cmol_err_t *err);
+
 int cmol__session_length(const cmol_session_t *s);
 int cmol__session_slot(const cmol_session_t *s);
 cmolhip_model_t *cmol__device(cmol_model_t *m);

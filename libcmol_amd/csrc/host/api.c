@@ -198,7 +198,9 @@ size_t cmol_arena_estimate(const char *path, const cmol_config_t *cfg)
 
 /* ---- load / free --------------------------------------------------------- */
 
-cmol_model_t *cmol_load(const char *path, const cmol_config_t *cfg, cmol_err_t *err)
+/* The load of cmol_load; with_device 0 stops after the tokenizer (no
+ * sessions, no device), for cmol__load_text. */
+static cmol_model_t *load_model(const char *path, const cmol_config_t *cfg, cmol_err_t *err, int with_device)
 {
     static const cmol_config_t def = CMOL_DEFAULT_CONFIG;
     cmol_err_t rc;
@@ -237,6 +239,10 @@ cmol_model_t *cmol_load(const char *path, const cmol_config_t *cfg, cmol_err_t *
     if (rc != CMOL_OK) FAIL(rc);
     rc = cmol_tokenizer_build(&m->tokenizer, &m->arena);
     if (rc != CMOL_OK) FAIL(rc);
+    if (!with_device) {
+        if (pthread_mutex_init(&m->pool_lock, NULL) != 0) FAIL(CMOL_ERR_OOM);
+        return m;
+    }
     m->session_slots = (struct cmol_session *)cmol_arena_alloc_n(&m->arena, (size_t)c.max_sessions,
                                                                  sizeof(struct cmol_session));
     if (!m->session_slots) FAIL(CMOL_ERR_OOM);
@@ -270,6 +276,16 @@ cmol_model_t *cmol_load(const char *path, const cmol_config_t *cfg, cmol_err_t *
              c.max_sessions, m->kv_f16 ? "f16" : "f32",
              cmolhip_arena_size(cmolhip_model_ctx(m->dev)));
     return m;
+}
+
+cmol_model_t *cmol_load(const char *path, const cmol_config_t *cfg, cmol_err_t *err)
+{
+    return load_model(path, cfg, err, 1);
+}
+
+cmol_model_t *cmol__load_text(const char *path, cmol_err_t *err)
+{
+    return load_model(path, NULL, err, 0);
 }
 
 void cmol_free(cmol_model_t *m)

@@ -4,7 +4,10 @@
  * Writes SmolLM-shaped GGUF v3 files that libcmol's loader accepts
  * (reference src/gguf.c:299-518): arch-prefixed UINT32/FLOAT32 hparams,
  * a tokenizer.ggml.tokens array, F32 norm weights, 32-byte data alignment,
- * output.weight omitted for tied embeddings.
+ * output.weight omitted for tied embeddings.  cmolsynth_write_gguf_tok adds a
+ * full tokenizer description (model, tokens, token types, merges, special
+ * ids, add-BOS flag) with the key types the reference reads
+ * (src/gguf.c:71-79,299-395).
  *
  * Weights are ~N(0, std) from a counter-based integer generator (sum of four
  * 16-bit uniforms from a splitmix64 hash, an Irwin-Hall approximation), so
@@ -283,7 +286,33 @@ static void vocab_string(int i, char *buf)
     else snprintf(buf, 16, "t%d", i);
 }
 
+/* Tokenizer of a synthetic model (all arrays of n_tokens entries; types and
+ * merges may be null; ids < 0 and add_bos < 0 are left out). */
+typedef struct {
+    const char *model;
+    int32_t n_tokens;
+    const char *const *tokens;
+    const int32_t *types;
+    int32_t n_merges;
+    const char *const *merges;
+    int32_t bos_id, eos_id, unk_id, add_bos;
+} cmolsynth_tok_t;
+
+static int write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads, const cmolsynth_tok_t *tk);
+
 int cmolsynth_write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads)
+{
+    return write_gguf(path, s, nthreads, NULL);
+}
+
+int cmolsynth_write_gguf_tok(const char *path, const cmolsynth_spec_t *s, int nthreads,
+                             const cmolsynth_tok_t *tk)
+{
+    if (!tk || !tk->model || !tk->tokens || tk->n_tokens != s->vocab) return -1;
+    return write_gguf(path, s, nthreads, tk);
+}
+
+static int write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads, const cmolsynth_tok_t *tk)
 {
     if (!path || !s || s->n_layers < 1 || s->d_model % 32 || s->d_ffn % 32 ||
         s->n_heads < 1 || s->d_model % s->n_heads || s->vocab < 1)
@@ -331,7 +360,12 @@ int cmolsynth_write_gguf(const char *path, const cmolsynth_spec_t *s, int nthrea
     FILE *f = fopen(path, "wb");
     if (!f) { free(td); return -2; }
     const char *arch = s->arch_smollm3 ? "smollm3" : "llama";
-    int n_kv = 12 + (s->nope_interval > 0) + (s->eos_id >= 0);
+    int n_kv = 12 + (s->nope_interval > 0);
+    if (tk)
+        n_kv += (tk->types != NULL) + (tk->n_merges > 0) + (tk->bos_id >= 0) + (tk->eos_id >= 0) +
+                (tk->unk_id >= 0) + (tk->add_bos >= 0);
+    else
+        n_kv += s->eos_id >= 0;
     w_u32(f, 0x46554747u);
     w_u32(f, 3);
     w_u64(f, (uint64_t)nt);
@@ -350,14 +384,46 @@ int cmolsynth_write_gguf(const char *path, const cmolsynth_spec_t *s, int nthrea
     kv_u32(f, AKEY("vocab_size"), (uint32_t)s->vocab);
     if (s->nope_interval > 0) kv_u32(f, AKEY("attention.no_rope_layer_interval"), (uint32_t)s->nope_interval);
 #undef AKEY
-    kv_str(f, "tokenizer.ggml.model", "llama");
-    if (s->eos_id >= 0) kv_u32(f, "tokenizer.ggml.eos_token_id", (uint32_t)s->eos_id);
-    /* token list */
-    w_str(f, "tokenizer.ggml.tokens");
-    w_u32(f, 9);
-    w_u32(f, 8);
-    w_u64(f, (uint64_t)s->vocab);
-    for (int i = 0; i < s->vocab; i++) { char vb[16]; vocab_string(i, vb); w_str(f, vb); }
+    if (!tk) {
+        kv_str(f, "tokenizer.ggml.model", "llama");
+        if (s->eos_id >= 0) kv_u32(f, "tokenizer.ggml.eos_token_id", (uint32_t)s->eos_id);
+        /* token list */
+        w_str(f, "tokenizer.ggml.tokens");
+        w_u32(f, 9);
+        w_u32(f, 8);
+        w_u64(f, (uint64_t)s->vocab);
+        for (int i = 0; i < s->vocab; i++) { char vb[16]; vocab_string(i, vb); w_str(f, vb); }
+    } else {
+        kv_str(f, "tokenizer.ggml.model", tk->model);
+        if (tk->bos_id >= 0) kv_u32(f, "tokenizer.ggml.bos_token_id", (uint32_t)tk->bos_id);
+        if (tk->eos_id >= 0) kv_u32(f, "tokenizer.ggml.eos_token_id", (uint32_t)tk->eos_id);
+        if (tk->unk_id >= 0) kv_u32(f, "tokenizer.ggml.unknown_token_id", (uint32_t)tk->unk_id);
+        if (tk->add_bos >= 0) {   /* BOOL */
+            w_str(f, "tokenizer.ggml.add_bos_token");
+            w_u32(f, 7);
+            uint8_t b = tk->add_bos ? 1 : 0;
+            fwrite(&b, 1, 1, f);
+        }
+        w_str(f, "tokenizer.ggml.tokens");   /* ARRAY of STRING */
+        w_u32(f, 9);
+        w_u32(f, 8);
+        w_u64(f, (uint64_t)tk->n_tokens);
+        for (int i = 0; i < tk->n_tokens; i++) w_str(f, tk->tokens[i]);
+        if (tk->types) {                     /* ARRAY of INT32 */
+            w_str(f, "tokenizer.ggml.token_type");
+            w_u32(f, 9);
+            w_u32(f, 5);
+            w_u64(f, (uint64_t)tk->n_tokens);
+            for (int i = 0; i < tk->n_tokens; i++) w_u32(f, (uint32_t)tk->types[i]);
+        }
+        if (tk->n_merges > 0) {              /* ARRAY of STRING */
+            w_str(f, "tokenizer.ggml.merges");
+            w_u32(f, 9);
+            w_u32(f, 8);
+            w_u64(f, (uint64_t)tk->n_merges);
+            for (int i = 0; i < tk->n_merges; i++) w_str(f, tk->merges[i]);
+        }
+    }
     /* tensor infos: shape[0] is the innermost (in-features) dimension */
     for (int i = 0; i < nt; i++) {
         w_str(f, td[i].name);

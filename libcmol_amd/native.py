@@ -113,6 +113,11 @@ SIGNATURES = [
     ("cmol__generate_ids", C.c_int, [P, P, C.c_int, C.POINTER(GenParams), P, C.c_int]),
     ("cmol__decode_batch", C.c_int, [P, P, C.c_int, P]),
     ("cmol__session_fill_kv", C.c_int, [P, C.c_int, C.c_uint64]),
+    ("cmol__load_text", P, [C.c_char_p, C.POINTER(C.c_int)]),
+    ("cmol_sample", I32, [P, C.c_int, C.POINTER(GenParams), P]),
+    ("cmol_rng_seed", None, [P, C.c_uint]),
+    ("cmol_rng_next", C.c_uint64, [P]),
+    ("cmol_apply_repeat_penalty", None, [P, C.c_int, P, C.c_int, C.c_float]),
     ("cmol__session_length", C.c_int, [P]),
     ("cmol__session_slot", C.c_int, [P]),
     ("cmol__device", P, [P]),
@@ -328,6 +333,52 @@ class Session:
 
     def fill_kv(self, n_tokens: int, seed: int = 7):
         check(lib().cmol__session_fill_kv(self.h, n_tokens, seed), "fill_kv")
+
+    def generate_text(self, prompt: bytes, params: GenParams):
+        """Public cmol_generate on a text prompt: the (piece, eos) pairs the
+        callback received, and the return code."""
+        got = []
+        cb = TOKEN_CB(lambda piece, n, eos, ud: got.append((C.string_at(piece, n), bool(eos))) or 0)
+        rc = lib().cmol_generate(self.h, prompt, C.byref(params), cb, None)
+        return got, rc
+
+
+def encode(h, text: bytes, cap: int = 8192):
+    """cmol_encode on model handle h: (ids, return code)."""
+    out = np.zeros(max(cap, 1), np.int32)
+    rc = lib().cmol_encode(h, text, ptr(out), cap)
+    return (out[:rc].copy() if rc >= 0 else None), rc
+
+
+def decode_token(h, tid: int) -> bytes | None:
+    return lib().cmol_decode_token(h, tid)
+
+
+class TextModel:
+    """A GGUF's tokenizer without a device (cmol__load_text)."""
+
+    def __init__(self, path: str):
+        err = C.c_int(0)
+        self.h = lib().cmol__load_text(path.encode(), C.byref(err))
+        if not self.h:
+            raise RuntimeError(f"cmol__load_text({path}) failed: {err.value}")
+
+    def encode(self, text: bytes, cap: int = 8192):
+        return encode(self.h, text, cap)
+
+    def decode_token(self, tid: int) -> bytes | None:
+        return decode_token(self.h, tid)
+
+    def close(self):
+        if self.h:
+            lib().cmol_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def decode_batch(sessions, tokens) -> np.ndarray:

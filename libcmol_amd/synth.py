@@ -28,6 +28,27 @@ class _Spec(C.Structure):
         ("norm_jitter", C.c_float), ("seed", C.c_uint64)]
 
 
+class _Tok(C.Structure):
+    _fields_ = [("model", C.c_char_p), ("n_tokens", C.c_int32), ("tokens", C.POINTER(C.c_char_p)),
+                ("types", C.POINTER(C.c_int32)), ("n_merges", C.c_int32),
+                ("merges", C.POINTER(C.c_char_p)), ("bos_id", C.c_int32), ("eos_id", C.c_int32),
+                ("unk_id", C.c_int32), ("add_bos", C.c_int32)]
+
+
+@dataclasses.dataclass(frozen=True)
+class Tokenizer:
+    """Tokenizer metadata of a synthetic GGUF (tokenizer.ggml.* keys); ids and
+    add_bos < 0 are left out of the file."""
+    model: str
+    tokens: tuple
+    types: tuple | None = None
+    merges: tuple = ()
+    bos_id: int = -1
+    eos_id: int = -1
+    unk_id: int = -1
+    add_bos: int = -1
+
+
 @dataclasses.dataclass(frozen=True)
 class ModelSpec:
     n_layers: int
@@ -103,6 +124,8 @@ def lib():
         L = C.CDLL(path)
         L.cmolsynth_write_gguf.argtypes = [C.c_char_p, C.POINTER(_Spec), C.c_int]
         L.cmolsynth_write_gguf.restype = C.c_int
+        L.cmolsynth_write_gguf_tok.argtypes = [C.c_char_p, C.POINTER(_Spec), C.c_int, C.POINTER(_Tok)]
+        L.cmolsynth_write_gguf_tok.restype = C.c_int
         L.cmolsynth_normal.argtypes = [C.c_void_p, C.c_int64, C.c_uint64, C.c_uint64, C.c_float]
         L.cmolsynth_tokens.argtypes = [C.c_void_p, C.c_int, C.c_uint64, C.c_int]
         L.cmolsynth_uniform.argtypes = [C.c_uint64, C.c_uint64]
@@ -121,6 +144,23 @@ def write_gguf(path: str, spec: ModelSpec, nthreads: int | None = None) -> str:
     rc = lib().cmolsynth_write_gguf(path.encode(), C.byref(s), nt)
     if rc != 0:
         raise RuntimeError(f"cmolsynth_write_gguf({path}) failed: {rc}")
+    return path
+
+
+def write_gguf_tok(path: str, spec: ModelSpec, tok: Tokenizer, nthreads: int | None = None) -> str:
+    """A synthetic model of `spec` whose tokenizer is `tok` (spec.vocab must be
+    len(tok.tokens))."""
+    enc = lambda xs: (C.c_char_p * len(xs))(*[x.encode("utf-8") for x in xs])
+    toks = enc(tok.tokens)
+    merges = enc(tok.merges) if tok.merges else None
+    types = (C.c_int32 * len(tok.types))(*tok.types) if tok.types is not None else None
+    t = _Tok(tok.model.encode(), len(tok.tokens), toks, types, len(tok.merges), merges,
+             tok.bos_id, tok.eos_id, tok.unk_id, tok.add_bos)
+    s = _Spec(**{f.name: getattr(spec, f.name) for f in dataclasses.fields(spec)})
+    nt = nthreads or min(16, os.cpu_count() or 1)
+    rc = lib().cmolsynth_write_gguf_tok(path.encode(), C.byref(s), nt, C.byref(t))
+    if rc != 0:
+        raise RuntimeError(f"cmolsynth_write_gguf_tok({path}) failed: {rc}")
     return path
 
 

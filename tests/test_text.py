@@ -1,0 +1,159 @@
+"""Text path against the reference (§8(f) first row): tokenizer encode and
+decode, the sampler, and cmol_generate on text prompts.
+
+Every expected value in tests/golden/text_golden.json was produced by the
+reference library built from its own sources (tests/golden/make_text_golden.py):
+cmol_encode / cmol_decode_token on two synthetic tokenizers (GPT-2 byte-level
+BPE, SentencePiece-style BPE with <0xNN> byte tokens), cmol_sample draws with
+cmol_rng_seed and cmol_apply_repeat_penalty, and cmol_generate's sampled ids.
+The fixture carries the tokenizers, so the GGUFs are rebuilt here with the
+synthetic-model writer.  Tokenizer and sampler checks run on the CPU (the
+text-only load needs no device); generation runs on the GPU."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import libcmol_amd.native as native
+from libcmol_amd import synth
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = json.load(open(os.path.join(HERE, "golden", "text_golden.json")))
+NAMES = sorted(GOLD["tokenizers"])
+
+
+def tokenizer_model(name, directory):
+    g = GOLD["tokenizers"][name]
+    t = g["tokenizer"]
+    tok = synth.Tokenizer(t["model"], tuple(t["tokens"]), tuple(t["types"]), tuple(t["merges"]),
+                          bos_id=t["bos_id"], eos_id=t["eos_id"], unk_id=t["unk_id"],
+                          add_bos=t["add_bos"])
+    sp = g["spec"]
+    spec = synth.ModelSpec(n_layers=sp["n_layers"], d_model=sp["d_model"], n_heads=sp["n_heads"],
+                           n_kv_heads=sp["n_kv_heads"], d_ffn=sp["d_ffn"], vocab=len(t["tokens"]),
+                           ctx_len=sp["ctx_len"], wtype=synth.Q8_0, embd_type=synth.Q8_0,
+                           wstd=sp["wstd"], seed=sp["seed"])
+    path = os.path.join(directory, f"text-{name}.gguf")
+    if not os.path.exists(path):
+        synth.write_gguf_tok(path, spec, tok)
+    return path
+
+
+@pytest.fixture(scope="module")
+def text_dir(tmp_path_factory):
+    return str(tmp_path_factory.mktemp("text"))
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_encode_matches_reference(text_dir, name):
+    """cmol_encode: the same ids (and return code) as the reference for every
+    text, including empty, whitespace runs, unicode, control-token strings and
+    characters that fall back to bytes or <unk>; a too-small buffer returns
+    the reference's error."""
+    m = native.TextModel(tokenizer_model(name, text_dir))
+    for case in GOLD["tokenizers"][name]["encode"]:
+        ids, rc = m.encode(case["text"].encode())
+        assert rc == case["rc"], repr(case["text"])
+        assert ids.tolist() == case["ids"], repr(case["text"])
+    _, rc = m.encode(b"the quick brown fox", cap=2)
+    assert rc == GOLD["tokenizers"][name]["encode_cap2_rc"]
+    m.close()
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_decode_token_matches_reference(text_dir, name):
+    """cmol_decode_token: the same bytes as the reference for every id (byte
+    tokens, U+2581 prefixes, GPT-2 byte-level characters, control tokens), and
+    NULL past the vocabulary."""
+    m = native.TextModel(tokenizer_model(name, text_dir))
+    pieces = GOLD["tokenizers"][name]["pieces"]
+    for i, want in enumerate(pieces):
+        got = m.decode_token(i)
+        assert (got.hex() if got is not None else None) == want, f"id {i}"
+    assert m.decode_token(len(pieces)) is None
+    assert m.decode_token(-1) is None
+    m.close()
+
+
+def sampler_logits(case_seed, draw, vocab):
+    """The fixture's logits: seeded, with exact ties every 7th entry."""
+    rng = np.random.default_rng([case_seed, draw])
+    x = (rng.standard_normal(vocab) * 3.0).astype(np.float32)
+    x[7::7] = x[6:-1:7][: x[7::7].size]
+    return x
+
+
+@pytest.mark.parametrize("ci", range(len(GOLD["sampler"]["cases"])))
+def test_sampler_matches_reference(ci):
+    """cmol_sample with cmol_rng_seed / cmol_apply_repeat_penalty: the same
+    draws as the reference for greedy, plain temperature, top-k (including
+    k = 1, k past the 512-entry buffer and k >= vocab), top-p and penalties,
+    on logits with exact ties."""
+    case = GOLD["sampler"]["cases"][ci]
+    V, L = GOLD["sampler"]["vocab"], native.lib()
+    prm = native.GenParams(case["temperature"], case["top_p"], case["top_k"], 0, case["seed"],
+                           case["penalty"], 64)
+    st = np.zeros(4, np.uint64)
+    L.cmol_rng_seed(st.ctypes.data, case["seed"])
+    hist = list(case["history"])
+    got = []
+    for d in range(GOLD["sampler"]["draws"]):
+        lg = sampler_logits(ci, d, V)
+        h = np.array(hist[-64:], np.int32)
+        L.cmol_apply_repeat_penalty(lg.ctypes.data, V, h.ctypes.data, h.size, case["penalty"])
+        tid = L.cmol_sample(lg.ctypes.data, V, prm, st.ctypes.data)
+        got.append(int(tid))
+        hist.append(int(tid))
+    assert got == case["ids"]
+
+
+def test_rng_stream_matches_closed_form():
+    """xoshiro256** seeded by splitmix64 (src/sampler.c:37-60): the first
+    outputs for seed 1 follow from the published recurrences, computed here
+    in Python integers."""
+    M = (1 << 64) - 1
+
+    def splitmix(x):
+        x = (x + 0x9E3779B97F4A7C15) & M
+        z = x
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return x, z ^ (z >> 31)
+
+    def rotl(v, k):
+        return ((v << k) | (v >> (64 - k))) & M
+
+    x, s = 1, []
+    for _ in range(4):
+        x, z = splitmix(x)
+        s.append(z)
+    want = []
+    for _ in range(6):
+        want.append((rotl((s[1] * 5) & M, 7) * 9) & M)
+        t = (s[1] << 17) & M
+        s[2] ^= s[0]; s[3] ^= s[1]; s[1] ^= s[2]; s[0] ^= s[3]; s[2] ^= t; s[3] = rotl(s[3], 45)
+    st = np.zeros(4, np.uint64)
+    native.lib().cmol_rng_seed(st.ctypes.data, 1)
+    got = [int(native.lib().cmol_rng_next(st.ctypes.data)) for _ in range(6)]
+    assert got == want
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", NAMES)
+def test_generate_text_matches_reference(gpu, text_dir, name):
+    """Public cmol_generate on text prompts (encode -> prefill -> decode ->
+    callback per piece), greedy with and without the repeat penalty: the
+    callback receives the decoded pieces of the reference's sampled ids."""
+    g = GOLD["tokenizers"][name]
+    pieces = [bytes.fromhex(p) for p in g["pieces"]]
+    m = native.Model(tokenizer_model(name, text_dir), max_ctx=128)
+    s = m.acquire()
+    for case in g["generate"]:
+        s.reset()
+        prm = native.default_params(temperature=0.0, max_new_tokens=case["max_new"], seed=0,
+                                    repeat_penalty=case["penalty"])
+        got, rc = s.generate_text(case["prompt"].encode(), prm)
+        assert rc == 0
+        assert [p for p, _ in got] == [pieces[i] for i in case["ids"]], case["prompt"]
+    m.close()
