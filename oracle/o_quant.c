@@ -39,7 +39,8 @@ float o_f16_to_f32(uint16_t h)
 }
 
 /* Block geometry per dtype: values per block, bytes per block.
- * Reference src/quant.c:298-308 (+ Q4_0, absent there: 18-byte blocks). */
+ * Reference src/quant.c:298-308 (+ Q4_0, absent there: 18-byte blocks);
+ * the K-quant super-blocks hold 256 values (src/quant.c:91-105). */
 int o_block_params(int dtype, size_t *bsz)
 {
     switch (dtype) {
@@ -48,6 +49,8 @@ int o_block_params(int dtype, size_t *bsz)
     case O_Q4_0: *bsz = 18; return 32;
     case O_Q5_0: *bsz = 22; return 32;
     case O_Q8_0: *bsz = 34; return 32;
+    case O_Q4_K: *bsz = 144; return 256;
+    case O_Q6_K: *bsz = 210; return 256;
     default:     *bsz = 0;  return 0;
     }
 }
@@ -98,12 +101,62 @@ static void deq_q4_0(const uint8_t *b, float *dst)
     }
 }
 
+/* Q4_K super-block: fp16 d, fp16 dmin, 12 bytes packing eight 6-bit
+ * scales and eight 6-bit mins, 128 bytes of nibbles.  Sub-block j takes
+ * scale/min j (j < 4: low 6 bits of bytes j / j+4; j >= 4: the low / high
+ * nibble of byte j+4 under the top two bits of bytes j-4 / j), and its 32
+ * values are the low (j even) or high (j odd) nibbles of bytes
+ * 32*(j/2) .. +31: value = (d*sc)*q - dmin*mn, products exact in fp32, one
+ * rounding at the subtraction.  src/quant.c:92-97,113-132,172-195 */
+static void q4k_scale_min(int j, const uint8_t *s, int *sc, int *mn)
+{
+    if (j < 4) {
+        *sc = s[j] & 0x3F;
+        *mn = s[j + 4] & 0x3F;
+    } else {
+        *sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        *mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static void deq_q4_k(const uint8_t *b, float *dst)
+{
+    float d = o_f16_to_f32(rd16(b)), dmin = o_f16_to_f32(rd16(b + 2));
+    for (int j = 0; j < 8; j++) {
+        int sc, mn;
+        q4k_scale_min(j, b + 4, &sc, &mn);
+        float db = d * (float)sc, mb = dmin * (float)mn;
+        const uint8_t *q = b + 16 + 32 * (j / 2);
+        int sh = (j & 1) ? 4 : 0;
+        for (int k = 0; k < 32; k++) dst[32 * j + k] = db * (float)((q[k] >> sh) & 0xF) - mb;
+    }
+}
+
+/* Q6_K super-block: ql[128], qh[64], int8 scales[16], fp16 d.  Value i (group
+ * g = i/32, j = i%32): low nibble of ql[(g<4 ? 0 : 64) + 32*(g&1) + j]
+ * (upper half when g&2), two high bits from qh[(g<4 ? 0 : 32) + j] at bit
+ * 2*(g&3); value = (d*scales[i/16]) * (q - 32).  src/quant.c:99-105,197-231 */
+static void deq_q6_k(const uint8_t *b, float *dst)
+{
+    float d = o_f16_to_f32(rd16(b + 208));
+    for (int i = 0; i < 256; i++) {
+        int g = i / 32, j = i % 32;
+        int lo = (b[(g < 4 ? 0 : 64) + (g & 1) * 32 + j] >> ((g & 2) ? 4 : 0)) & 0xF;
+        int hi = (b[128 + (g < 4 ? 0 : 32) + j] >> ((g & 3) * 2)) & 0x3;
+        int q = (lo | (hi << 4)) - 32;
+        dst[i] = d * (float)(int8_t)b[192 + i / 16] * (float)q;
+    }
+}
+
+/* One block (32 values, or 256 for the K-quants) into dst. */
 static void deq_block(const uint8_t *b, float *dst, int dtype)
 {
     switch (dtype) {
     case O_Q4_0: deq_q4_0(b, dst); break;
     case O_Q5_0: deq_q5_0(b, dst); break;
     case O_Q8_0: deq_q8_0(b, dst); break;
+    case O_Q4_K: deq_q4_k(b, dst); break;
+    case O_Q6_K: deq_q6_k(b, dst); break;
     default: break;
     }
 }
@@ -120,10 +173,10 @@ void o_dequant_row(const void *src, float *dst, int n, int dtype)
     case O_F16:
         for (int i = 0; i < n; i++) dst[i] = o_f16_to_f32(rd16(s + 2 * i));
         break;
-    case O_Q4_0: case O_Q5_0: case O_Q8_0: {
+    case O_Q4_0: case O_Q5_0: case O_Q8_0: case O_Q4_K: case O_Q6_K: {
         size_t bsz;
-        o_block_params(dtype, &bsz);
-        for (int bi = 0; bi < n / 32; bi++) deq_block(s + bi * bsz, dst + bi * 32, dtype);
+        int bs = o_block_params(dtype, &bsz);
+        for (int bi = 0; bi < n / bs; bi++) deq_block(s + bi * bsz, dst + bi * bs, dtype);
         break;
     }
     default:
@@ -159,7 +212,7 @@ void o_matmul(float *out, const void *a, const float *b,
     if (!bs) return;
     const uint8_t *ab = (const uint8_t *)a;
     size_t row_bytes = (size_t)(k / bs) * bsz;
-    float tmp[32];
+    float tmp[256];
 
     for (int mi = 0; mi < m; mi++) {
         const uint8_t *row = ab + (size_t)mi * row_bytes;
@@ -176,10 +229,10 @@ void o_matmul(float *out, const void *a, const float *b,
             }
             if (order == O_ORDER_SCALAR) {
                 float acc = 0.0f;
-                for (int bi = 0; bi < k / 32; bi++) {
+                for (int bi = 0; bi < k / bs; bi++) {
                     deq_block(row + bi * bsz, tmp, dtype);
-                    for (int j = 0; j < 32; j++)
-                        acc = acc + tmp[j] * b[(size_t)(bi * 32 + j) * n + ni];
+                    for (int j = 0; j < bs; j++)
+                        acc = acc + tmp[j] * b[(size_t)(bi * bs + j) * n + ni];
                 }
                 out[(size_t)mi * n + ni] = acc;
                 continue;
@@ -197,11 +250,11 @@ void o_matmul(float *out, const void *a, const float *b,
                 out[(size_t)mi * n + ni] = t;
                 continue;
             }
-            for (int bi = 0; bi < k / 32; bi++) {
+            for (int bi = 0; bi < k / bs; bi++) {
                 deq_block(row + bi * bsz, tmp, dtype);
-                for (int h = 0; h < 32; h += 16)
+                for (int h = 0; h < bs; h += 16)
                     for (int j = 0; j < 16; j++)
-                        lane[j] = fmaf(tmp[h + j], b[(size_t)(bi * 32 + h + j) * n + ni], lane[j]);
+                        lane[j] = fmaf(tmp[h + j], b[(size_t)(bi * bs + h + j) * n + ni], lane[j]);
             }
             out[(size_t)mi * n + ni] = reduce16(lane);
         }

@@ -35,7 +35,7 @@ extern "C" {
 #endif
 
 /* GGUF dtype tags used on the path (reference src/cmol_internal.h:27-37). */
-enum { O_F32 = 0, O_F16 = 1, O_Q4_0 = 2, O_Q5_0 = 6, O_Q8_0 = 8 };
+enum { O_F32 = 0, O_F16 = 1, O_Q4_0 = 2, O_Q5_0 = 6, O_Q8_0 = 8, O_Q4_K = 12, O_Q6_K = 14 };
 
 /* Matmul accumulation orders of the reference kernels. */
 enum { O_ORDER_SCALAR = 0,   /* cmol_matmul_scalar  src/quant.c:334-376 */

@@ -103,6 +103,73 @@ def test_q5_0_closed_form():
     assert np.array_equal(bits(got), bits(want))
 
 
+# ---- K-quants (tests/golden/make_kquant_golden.py) ---------------------------
+KQ = np.load(os.path.join(HERE, "golden", "kquant.npz"))
+
+
+@pytest.mark.parametrize("name,dt", [("q4_k", 12), ("q6_k", 14)])
+@pytest.mark.parametrize("tag", ["rand", "special"])
+def test_kquant_dequant_matches_reference(name, dt, tag):
+    raw = KQ[f"deq_{name}_{tag}_raw"]
+    want = KQ[f"deq_{name}_{tag}_out"]
+    cols = want.shape[1]
+    got = np.stack([O.dequant_row(raw[r], cols, dt) for r in range(raw.shape[0])])
+    assert np.array_equal(bits(got), want)
+
+
+@pytest.mark.parametrize("name,dt", [("q4_k", 12), ("q6_k", 14)])
+@pytest.mark.parametrize("shape", [(16, 512, 1), (24, 768, 3)])
+def test_kquant_matmul_matches_reference_orders(name, dt, shape):
+    m, k, n = shape
+    key = f"mm_{name}_{m}x{k}x{n}"
+    a, b = KQ[key + "_raw"], KQ[key + "_b"]
+    for order, suffix in ((O.SCALAR, "_scalar"), (O.AVX512, "_avx512")):
+        assert np.array_equal(bits(O.matmul(a, b, m, k, dt, order)), KQ[key + suffix]), suffix
+
+
+def test_q4_k_closed_form():
+    """Q4_K: sub-block j of a super-block with d = 1, dmin = 0.5, scale
+    j + 1 and min 2j (the six-bit packing spelled out by hand, bits 4-5 of
+    scales/mins 4..7 in the top bits of bytes 0..7) and codes q = (k + j) % 16
+    dequantises to (j + 1) q - j."""
+    sc = [j + 1 for j in range(8)]
+    mn = [2 * j for j in range(8)]
+    s = np.zeros(12, np.uint8)
+    for j in range(4):
+        s[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    q = np.array([[(k + j) % 16 for k in range(32)] for j in range(8)], np.uint8)
+    qs = np.zeros(128, np.uint8)
+    for p in range(4):
+        qs[32 * p:32 * p + 32] = q[2 * p] | (q[2 * p + 1] << 4)
+    blk = np.concatenate([np.frombuffer(np.float16(1.0).tobytes(), np.uint8),
+                          np.frombuffer(np.float16(0.5).tobytes(), np.uint8), s, qs])
+    got = O.dequant_row(blk, 256, 12).reshape(8, 32)
+    want = np.array([[(j + 1) * q[j, k] - 0.5 * (2 * j) for k in range(32)] for j in range(8)], np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_q6_k_closed_form():
+    """Q6_K: value i of a super-block with d = 0.25 and int8 scale
+    (i//16) - 8 holds code c = (7 i) % 64 split into ql nibbles and qh bit
+    pairs as the reference lays them out; it dequantises to
+    0.25 (i//16 - 8)(c - 32)."""
+    c = np.array([(7 * i) % 64 for i in range(256)])
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for i in range(256):
+        g, j = divmod(i, 32)
+        li = (0 if g < 4 else 64) + 32 * (g & 1) + j
+        ql[li] |= (c[i] & 0xF) << (4 if g & 2 else 0)
+        qh[(0 if g < 4 else 32) + j] |= (c[i] >> 4) << (2 * (g & 3))
+    scales = np.array([k - 8 for k in range(16)], np.int8).view(np.uint8)
+    blk = np.concatenate([ql, qh, scales, np.frombuffer(np.float16(0.25).tobytes(), np.uint8)])
+    got = O.dequant_row(blk, 256, 14)
+    want = np.array([0.25 * (i // 16 - 8) * (c[i] - 32) for i in range(256)], np.float32)
+    assert np.array_equal(got, want)
+
+
 # ---- matmul -------------------------------------------------------------------
 @pytest.mark.parametrize("name,dt", [("q8_0", 8), ("q5_0", 6), ("q4_0", 2)])
 @pytest.mark.parametrize("shape", [(16, 128, 1), (33, 256, 1), (8, 64, 3)])
