@@ -57,17 +57,20 @@ struct QLayout {
     int rt, bq;
 };
 
+// Byte sizes of the tiled arrays: codes, scales (4 fp16 per column per cell,
+// or a 16-byte record per column per cell for the K-quants), and the Q5_0
+// fifth bits / Q6_K high bits.
 bool qlayout(int dtype, int rows, int cols, int fold, QLayout *L)
 {
-    if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0) return false;
-    if (rows <= 0 || cols <= 0 || cols % 32 || !fold_ok(fold)) return false;
+    if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0 && !is_kquant(dtype)) return false;
+    if (rows <= 0 || cols <= 0 || cols % block_values_of(dtype) || !fold_ok(fold)) return false;
     const int R = 16 / fold;
     L->rt = (rows + R - 1) / R;
     L->bq = fold_quads(cols / 32, fold);
     size_t cells = (size_t)L->rt * L->bq;
     L->qs = cells * 64 * lane_bytes_of(dtype);
-    L->d = cells * 64 * 2;
-    L->qh = dtype == DT_Q5_0 ? cells * 64 * 4 : 0;
+    L->d = is_kquant(dtype) ? cells * 16 * 16 : cells * 64 * 2;
+    L->qh = dtype == DT_Q5_0 ? cells * 64 * 4 : dtype == DT_Q6_K ? cells * 64 * 8 : 0;
     return true;
 }
 
@@ -96,7 +99,7 @@ QTensor to_qt(const cmolhip_qtensor_t &t)
 size_t raw_row_bytes(int dtype, int cols)
 {
     int bb = block_bytes_of(dtype);
-    return bb ? (size_t)(cols / 32) * bb : 0;
+    return bb ? (size_t)(cols / block_values_of(dtype)) * bb : 0;
 }
 
 } // namespace
@@ -288,7 +291,7 @@ int cmolhip_act_prepare(cmolhip_ctx_t *c, const float *dx, int n, int cols, int 
                         const float *norm_w, void *op, float *ss)
 {
     if (!c || !dx || !op || n < 1 || n > GEMM_MAX_N || cols < 32 || cols % 32) return E_ARGS;
-    if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0) return E_UNSUPPORTED;
+    if (dtype != DT_Q4_0 && dtype != DT_Q5_0 && dtype != DT_Q8_0 && !is_kquant(dtype)) return E_UNSUPPORTED;
     ActOut o{};
     o.q = (_Float16 *)op;
     o.dt = dtype;
@@ -514,7 +517,7 @@ int pick_split(int max_ctx)
     return s;
 }
 
-bool is_block_fmt(int dt) { return dt == DT_Q4_0 || dt == DT_Q5_0 || dt == DT_Q8_0; }
+bool is_block_fmt(int dt) { return dt == DT_Q4_0 || dt == DT_Q5_0 || dt == DT_Q8_0 || is_kquant(dt); }
 
 // Byte sizes of everything the model puts in the arena, in creation order.
 struct Plan {
@@ -580,6 +583,7 @@ int persist_format(const cmolhip_model_desc_t *d)
     const cmolhip_hparams_t &h = d->hp;
     if (h.max_sessions != 1 || (h.d_head != 64 && h.d_head != 128)) return 0;
     const int dt = d->layers[0].q.dtype;
+    if (dt != DT_Q4_0 && dt != DT_Q5_0 && dt != DT_Q8_0) return 0;   // no K-quant kernel
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &L = d->layers[l];
         if (L.q.dtype != dt || L.o.dtype != dt || L.gate.dtype != dt || L.down.dtype != dt) return 0;

@@ -12,7 +12,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-enum { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q5_0 = 6, DT_Q8_0 = 8 };
+enum { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q5_0 = 6, DT_Q8_0 = 8, DT_Q4_K = 12, DT_Q6_K = 14 };
 
 // Global-memory view of a generic pointer: accesses through the result
 // compile to global_* instructions.  Used where the compiler cannot infer the
@@ -64,8 +64,21 @@ __device__ __forceinline__ T ldg(const T *p)
 //
 // k order inside a block for lane group g, element e (the same permutation is
 // applied to the activation operand, so the MFMA contraction is unchanged):
-//   Q4_0/Q5_0: e -> (e>=4 ? 16 : 0) + 4g + {0,2,1,3}[e&3]
-//   Q8_0:      e -> 8g + e
+//   Q4_0/Q5_0/Q4_K/Q6_K: e -> (e>=4 ? 16 : 0) + 4g + {0,2,1,3}[e&3]
+//   Q8_0:                e -> 8g + e
+//
+// K-quants (super-blocks of 256 = 8 blocks of 32, so a quad never straddles
+// two super-blocks): the "blocks" above are the 32-value sub-blocks.
+//   Q4_K: codes as Q4_0 (nibble q, decoded as q - 8); no fifth-bit array.
+//   Q6_K: low nibbles as Q4_0; the two high bits of the lane's 8 codes of a
+//         block in 16 bits (bits 2p..2p+1: low element of pair p, bits
+//         8+2p..: high element, pairs as deq_q4 orders them), two blocks per
+//         dword, two dwords per lane per cell.
+//   Scales: a 16-byte record per (cell, column) instead of 4 fp16 scales:
+//     Q4_K: [d | dmin << 16, sc0 mn0 sc1 mn1, sc2 mn2 sc3 mn3, 0] (fp16 bits,
+//           then the cell's four 6-bit scale/min pairs as bytes);
+//     Q6_K: [d, s0 s0' s1 s1', s2 s2' s3 s3', 0] (int8 scales of the low and
+//           high 16 values of each block).
 // ---------------------------------------------------------------------------
 
 __host__ __device__ inline bool fold_ok(int f) { return f == 1 || f == 2 || f == 4 || f == 8; }
@@ -76,12 +89,18 @@ template <int DT> struct QFmt;
 template <> struct QFmt<DT_Q4_0> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 18; };
 template <> struct QFmt<DT_Q5_0> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 22; };
 template <> struct QFmt<DT_Q8_0> { static constexpr int LANE_BYTES = 32, BLOCK_BYTES = 34; };
+template <> struct QFmt<DT_Q4_K> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 144; };
+template <> struct QFmt<DT_Q6_K> { static constexpr int LANE_BYTES = 16, BLOCK_BYTES = 210; };
 
+__host__ __device__ constexpr bool is_kquant(int dt) { return dt == DT_Q4_K || dt == DT_Q6_K; }
 __host__ __device__ inline int lane_bytes_of(int dt) { return dt == DT_Q8_0 ? 32 : 16; }
+// bytes of one GGUF block (a 256-value super-block for the K-quants)
 __host__ __device__ inline int block_bytes_of(int dt)
 {
-    return dt == DT_Q4_0 ? 18 : dt == DT_Q5_0 ? 22 : dt == DT_Q8_0 ? 34 : 0;
+    return dt == DT_Q4_0 ? 18 : dt == DT_Q5_0 ? 22 : dt == DT_Q8_0 ? 34 : dt == DT_Q4_K ? 144
+         : dt == DT_Q6_K ? 210 : 0;
 }
+__host__ __device__ inline int block_values_of(int dt) { return is_kquant(dt) ? 256 : 32; }
 
 // position (0..31) inside a block of element e for lane group g
 __host__ __device__ inline int kmap(int dt, int g, int e)
@@ -150,6 +169,25 @@ __device__ inline f16x8 deq_q5(uint32_t D, uint32_t hb)
                  as_h2(p3) * s16 + bias16);
 }
 
+// Q6_K: nibbles as Q4_0 plus two high bits per code; hq = the lane's 16
+// bits for this block (see the layout notes).  value = (nibble | hi << 4) - 32;
+// 1024 + 16 * 63 < 2048 keeps the upper-nibble halves exact.
+__device__ inline f16x8 deq_q6(uint32_t D, uint32_t hq)
+{
+    const uint32_t m = magic_1024();
+    const f16x2 bias = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const f16x2 bias16 = {(_Float16)-96.0f, (_Float16)-96.0f};
+    const uint32_t x = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
+    const uint32_t Dh = D >> 8;
+    const uint32_t p0 = (D & 0x000F000Fu) | m | ((x << 4) & 0x00300030u);
+    const uint32_t p1 = (Dh & 0x000F000Fu) | m | ((x << 2) & 0x00300030u);
+    const uint32_t p2 = (D & 0x00F000F0u) | m | ((x << 4) & 0x03000300u);
+    const uint32_t p3 = (Dh & 0x00F000F0u) | m | ((x << 2) & 0x03000300u);
+    return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) * s16 + bias16,
+                 as_h2(p3) * s16 + bias16);
+}
+
 // Q8_0: two dwords of int8 codes; flip the sign bit (b+128 in 0..255),
 // place each byte under the 0x64 exponent byte, subtract 1152.
 __device__ inline f16x8 deq_q8(uint32_t D0, uint32_t D1)
@@ -164,12 +202,15 @@ __device__ inline f16x8 deq_q8(uint32_t D0, uint32_t D1)
     return pack8(as_h2(p0) + bias, as_h2(p1) + bias, as_h2(p2) + bias, as_h2(p3) + bias);
 }
 
-// Decoded codes of block bi (0..3) of a quad from a lane's loaded data.
+// Decoded codes of block bi (0..3) of a quad from a lane's loaded data (h:
+// Q5_0 fifth bits; Q6_K high bits of blocks 0,1 (c1[0]) and 2,3 (c1[1])).
 template <int DT>
 __device__ inline f16x8 deq_block(const u32x4 c0, const u32x4 c1, uint32_t h, int bi)
 {
-    if constexpr (DT == DT_Q4_0) {
+    if constexpr (DT == DT_Q4_0 || DT == DT_Q4_K) {
         return deq_q4(c0[bi]);
+    } else if constexpr (DT == DT_Q6_K) {
+        return deq_q6(c0[bi], (c1[bi >> 1] >> (16 * (bi & 1))) & 0xFFFFu);
     } else if constexpr (DT == DT_Q5_0) {
         return deq_q5(c0[bi], (h >> (8 * bi)) & 0xFFu);
     } else {
@@ -203,6 +244,33 @@ __device__ inline float mul_scale_x86(float d, float q)
         if (q == 0.0f) return __uint_as_float(0xFFC00000u);
     }
     return d * q;
+}
+
+// x86 SSE multiply / subtract (first operand a): a NaN operand comes out
+// quieted, a's before b's; an invalid operation (inf * 0, inf - inf) gives
+// the default NaN 0xFFC00000.  Used where the reference's dequantised values
+// are matched bit for bit, special scales included.
+__device__ inline bool nan_bits(float a) { return (__float_as_uint(a) & 0x7FFFFFFFu) > 0x7F800000u; }
+__device__ inline float quieted(float a) { return __uint_as_float(__float_as_uint(a) | 0x00400000u); }
+__device__ inline bool inf_bits(float a) { return (__float_as_uint(a) & 0x7FFFFFFFu) == 0x7F800000u; }
+
+__device__ inline float mul_x86(float a, float b)
+{
+#pragma clang fp contract(off)
+    if (nan_bits(a)) return quieted(a);
+    if (nan_bits(b)) return quieted(b);
+    if ((inf_bits(a) && b == 0.0f) || (inf_bits(b) && a == 0.0f)) return __uint_as_float(0xFFC00000u);
+    return a * b;
+}
+
+__device__ inline float sub_x86(float a, float b)
+{
+#pragma clang fp contract(off)
+    if (nan_bits(a)) return quieted(a);
+    if (nan_bits(b)) return quieted(b);
+    if (inf_bits(a) && inf_bits(b) && ((__float_as_uint(a) ^ __float_as_uint(b)) & 0x80000000u) == 0)
+        return __uint_as_float(0xFFC00000u);
+    return a - b;
 }
 
 // ---- reductions ------------------------------------------------------------

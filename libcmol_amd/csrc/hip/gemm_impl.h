@@ -34,7 +34,6 @@ struct GemmShape {
 template <int DT>
 __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape sh)
 {
-    constexpr int LB = QFmt<DT>::LANE_BYTES;
     constexpr int ASTAGE = 4 * 4 * 2 * GEMM_BM * 16;   // [block][k-group][128 rows][16 B]
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *s_a = smem;                                 // GEMM_STAGES x ASTAGE
@@ -78,7 +77,7 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
     }
 
     u32x4 c0[GEMM_STAGES][2], c1[GEMM_STAGES][2];
-    u32x2 dv[GEMM_STAGES][2];
+    typename QScale<DT>::T dv[GEMM_STAGES][2];
     uint32_t hv[GEMM_STAGES][2];
     // loads of quad kk into stage st: 4 operand copies (of the tile's 32
     // 1 KiB pieces) and the codes/scales of the wave's two virtual tiles;
@@ -103,16 +102,10 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
         for (int j = 0; j < 2; j++) {
             const size_t cell = (size_t)wt[j] * BQ + q;
             const int col = p * R + wc[j];
-            const u32x4 *src = (const u32x4 *)(a.w.qs + (cell * 64 + col + 16 * g) * LB);
-            c0[st][j] = src[0];
-            if constexpr (LB == 32) c1[st][j] = src[1];
-            else c1[st][j] = u32x4{0, 0, 0, 0};
-            dv[st][j] = *(const u32x2 *)(a.w.d + cell * 64 + col * 4);
-            if constexpr (DT == DT_Q5_0) hv[st][j] = a.w.qh[cell * 64 + col + 16 * g];
-            else hv[st][j] = 0u;
+            q_load<DT>(a.w, cell, col, col + 16 * g, c0[st][j], c1[st][j], dv[st][j], hv[st][j]);
         }
     };
-    constexpr int LPS = 4 + 2 * ((LB == 32 ? 2 : 1) + 1 + (DT == DT_Q5_0 ? 1 : 0));
+    constexpr int LPS = 4 + 2 * q_loads<DT>();
 
     const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc[4][2];
@@ -132,24 +125,17 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
         for (int bi = 0; bi < 4; bi++) {
             if (bi >= nb) break;
             f16x8 wv[2];
-            float dsc[2];
+            BlockScale bs[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 wv[j] = deq_block<DT>(c0[st][j], c1[st][j], hv[st][j], bi);
-                const uint32_t dw = dv[st][j][bi >> 1];
-                dsc[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)((bi & 1) ? (dw >> 16) : (dw & 0xFFFFu)));
+                bs[j] = block_scale<DT>(dv[st][j], bi);
             }
 #pragma unroll
             for (int gi = 0; gi < 4; gi++) {
                 const f16x8 xv = *(const f16x8 *)&sa[((bi * 4 + g) * 2 * GEMM_BM + 64 * wm + 16 * gi + cl) * 16];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv[j], zero4, 0, 0, 0);
-                    acc[gi][j][0] = fmaf(dsc[j], cc[0], acc[gi][j][0]);
-                    acc[gi][j][1] = fmaf(dsc[j], cc[1], acc[gi][j][1]);
-                    acc[gi][j][2] = fmaf(dsc[j], cc[2], acc[gi][j][2]);
-                    acc[gi][j][3] = fmaf(dsc[j], cc[3], acc[gi][j][3]);
-                }
+                for (int j = 0; j < 2; j++) mfma_block<DT>(acc[gi][j], xv, wv[j], bs[j]);
             }
         }
     };

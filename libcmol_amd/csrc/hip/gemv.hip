@@ -1,6 +1,6 @@
 // gemv.hip — quantised matvec / small-batch GEMM for gfx950.
 //
-// y[n] = W . x[n] for a Q4_0/Q5_0/Q8_0 weight in the quad-tile layout and up
+// y[n] = W . x[n] for a Q4_0/Q5_0/Q8_0/Q4_K/Q6_K weight in the quad-tile layout and up
 // to 32 activation vectors (kernel template in gemv_impl.h).  One work-group
 // owns one 16-row tile and its NW wavefronts split the k range.  The
 // activation operand of the whole k range is copied into LDS once with
@@ -29,6 +29,10 @@ int launch_gemv_q8(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemm_q4(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemm_q5(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemm_q8(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemv_q4k(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemv_q6k(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemm_q4k(const GemvArgs &a, int epi, hipStream_t s);
+int launch_gemm_q6k(const GemvArgs &a, int epi, hipStream_t s);
 
 size_t act_bytes(int K, int n)
 {
@@ -45,6 +49,8 @@ int launch_gemv(const GemvArgs &a, int epi, hipStream_t s)
     case DT_Q4_0: rc = launch_gemv_q4(a, epi, s); break;
     case DT_Q5_0: rc = launch_gemv_q5(a, epi, s); break;
     case DT_Q8_0: rc = launch_gemv_q8(a, epi, s); break;
+    case DT_Q4_K: rc = launch_gemv_q4k(a, epi, s); break;
+    case DT_Q6_K: rc = launch_gemv_q6k(a, epi, s); break;
     default: return -4;
     }
     if (rc) return rc;
@@ -59,6 +65,8 @@ int launch_gemm(const GemvArgs &a, int epi, hipStream_t s)
     case DT_Q4_0: rc = launch_gemm_q4(a, epi, s); break;
     case DT_Q5_0: rc = launch_gemm_q5(a, epi, s); break;
     case DT_Q8_0: rc = launch_gemm_q8(a, epi, s); break;
+    case DT_Q4_K: rc = launch_gemm_q4k(a, epi, s); break;
+    case DT_Q6_K: rc = launch_gemm_q6k(a, epi, s); break;
     default: return -4;
     }
     if (rc) return rc;

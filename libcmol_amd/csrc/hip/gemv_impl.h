@@ -277,12 +277,11 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
 template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI>
 __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
 {
-    constexpr int LB = QFmt<DT>::LANE_BYTES;
     // launch arguments needed before the weight loads go out, fetched in
     // one round trip
     sgpr_pin(a.w.qs);
     sgpr_pin(a.w.d);
-    if constexpr (DT == DT_Q5_0) sgpr_pin(a.w.qh);
+    if constexpr (DT == DT_Q5_0 || DT == DT_Q6_K) sgpr_pin(a.w.qh);
     sgpr_pin(a.w.rows);
     sgpr_pin(a.w.cols);
     sgpr_pin(a.w.block_quads);
@@ -337,7 +336,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     // elements past the wave's run re-read its last quad so every slot is
     // loaded unconditionally and the load counters stay exact ----
     u32x4 c0[U], c1[U];
-    u32x2 dv[U];
+    typename QScale<DT>::T dv[U];
     uint32_t hv[U];
     auto quad_of = [&](int i) {
         i = min(i, len - 1);
@@ -345,14 +344,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
         return min(c * cq + wid * qpc + (i - c * qpc), BQ - 1);
     };
     auto load_slot = [&](int u, int i) {
-        const size_t cell = cell0 + quad_of(i);
-        const u32x4 *p = (const u32x4 *)(a.w.qs + (cell * 64 + l) * LB);
-        c0[u] = p[0];
-        if constexpr (LB == 32) c1[u] = p[1];
-        else c1[u] = u32x4{0, 0, 0, 0};
-        dv[u] = *(const u32x2 *)(a.w.d + cell * 64 + (l & 15) * 4);
-        if constexpr (DT == DT_Q5_0) hv[u] = a.w.qh[cell * 64 + l];
-        else hv[u] = 0u;
+        q_load<DT>(a.w, cell0 + quad_of(i), l & 15, l, c0[u], c1[u], dv[u], hv[u]);
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load_slot(u, u);
@@ -362,8 +354,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     // (loads retire in issue order: every load but the ring's) and meet ----
     if constexpr (!CHUNKED) lds_zero<NW>(s_op + nblk * vb, sh.zslot + 16 - nblk * vb, threadIdx.x);
     else lds_zero<NW>(s_op + sh.zslot, 16, threadIdx.x);
-    // load instructions per ring slot: codes (1 or 2) + scales (+ fifth bits)
-    constexpr int LPS = (LB == 32 ? 2 : 1) + 1 + (DT == DT_Q5_0 ? 1 : 0);
+    // load instructions per ring slot
+    constexpr int LPS = q_loads<DT>();
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(LPS * U));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -408,22 +400,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
             for (int gi = 0; gi < NG; gi++)
                 xv[bi][gi] = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
         }
-        const float dsc[4] = {
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] & 0xFFFFu)),
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] >> 16)),
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] & 0xFFFFu)),
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] >> 16))};
 #pragma unroll
         for (int bi = 0; bi < 4; bi++) {
             const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
+            const BlockScale bs = block_scale<DT>(dv[u], bi);
 #pragma unroll
-            for (int gi = 0; gi < NG; gi++) {
-                const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[bi][gi], wv, zero4, 0, 0, 0);
-                acc[gi][0] = fmaf(dsc[bi], cc[0], acc[gi][0]);
-                acc[gi][1] = fmaf(dsc[bi], cc[1], acc[gi][1]);
-                acc[gi][2] = fmaf(dsc[bi], cc[2], acc[gi][2]);
-                acc[gi][3] = fmaf(dsc[bi], cc[3], acc[gi][3]);
-            }
+            for (int gi = 0; gi < NG; gi++) mfma_block<DT>(acc[gi], xv[bi][gi], wv, bs);
         }
     };
     // rounds of U: while another round follows, slot u is refilled right
@@ -714,7 +696,6 @@ template <int DT, int U>
 __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
 {
 #pragma clang fp contract(off)
-    constexpr int LB = QFmt<DT>::LANE_BYTES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int BQ = a.w.block_quads, nblk = a.w.cols >> 5, T = a.w.row_tiles;
     const int b = blockIdx.x;
@@ -750,19 +731,12 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
     const int ntw = max(0, min(sh.tpw, T - t0));
     const int len = ntw * nq;
     u32x4 c0[U], c1[U];
-    u32x2 dv[U];
+    typename QScale<DT>::T dv[U];
     uint32_t hv[U];
     auto load_slot = [&](int u, int i) {
         i = min(i, len - 1);
         const int j = i / nq, q = i - j * nq;
-        const size_t cell = (size_t)(t0 + j) * BQ + q0 + q;
-        const u32x4 *p = (const u32x4 *)(a.w.qs + (cell * 64 + l) * LB);
-        c0[u] = p[0];
-        if constexpr (LB == 32) c1[u] = p[1];
-        else c1[u] = u32x4{0, 0, 0, 0};
-        dv[u] = *(const u32x2 *)(a.w.d + cell * 64 + (l & 15) * 4);
-        if constexpr (DT == DT_Q5_0) hv[u] = a.w.qh[cell * 64 + l];
-        else hv[u] = 0u;
+        q_load<DT>(a.w, (size_t)(t0 + j) * BQ + q0 + q, l & 15, l, c0[u], c1[u], dv[u], hv[u]);
     };
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -810,21 +784,12 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
         acc = zero4;
     };
     auto compute = [&](int u, int i) {
-        const float dsc[4] = {
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] & 0xFFFFu)),
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][0] >> 16)),
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] & 0xFFFFu)),
-            (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[u][1] >> 16))};
         const int j = i / nq, q = i - j * nq;
 #pragma unroll
         for (int bi = 0; bi < 4; bi++) {
             const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
             const f16x8 xv = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
-            const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, zero4, 0, 0, 0);
-            acc[0] = fmaf(dsc[bi], cc[0], acc[0]);
-            acc[1] = fmaf(dsc[bi], cc[1], acc[1]);
-            acc[2] = fmaf(dsc[bi], cc[2], acc[2]);
-            acc[3] = fmaf(dsc[bi], cc[3], acc[3]);
+            mfma_block<DT>(acc, xv, wv, block_scale<DT>(dv[u], bi));
         }
         if (q == nq - 1) finish_tile(j);
     };

@@ -15,6 +15,104 @@ struct QTensor {
     int dtype, rows, cols, row_tiles, block_quads, fold;
 };
 
+// ---------------------------------------------------------------------------
+// Per-format lane data of one (cell, lane) and the per-block contraction,
+// shared by the matvec, batched matvec and GEMM kernels.
+// ---------------------------------------------------------------------------
+// Scales of a cell's column: 4 fp16 (32-value blocks) or the K-quant record.
+template <int DT> struct QScale { typedef u32x2 T; };
+template <> struct QScale<DT_Q4_K> { typedef u32x4 T; };
+template <> struct QScale<DT_Q6_K> { typedef u32x4 T; };
+
+// Load instructions per (cell, lane): codes (1, or 2 for Q8_0) + scales +
+// Q5_0 fifth bits / Q6_K high bits.
+template <int DT>
+constexpr int q_loads()
+{
+    return (DT == DT_Q8_0 ? 2 : 1) + 1 + (DT == DT_Q5_0 || DT == DT_Q6_K ? 1 : 0);
+}
+
+// Codes of lane `lane` and scales of column `col` of cell `cell`: c1 holds
+// the second half of the Q8_0 codes or the Q6_K high bits (.x blocks 0-1, .y
+// blocks 2-3); h the Q5_0 fifth bits.
+template <int DT>
+__device__ __forceinline__ void q_load(const QTensor &w, size_t cell, int col, int lane, u32x4 &c0,
+                                       u32x4 &c1, typename QScale<DT>::T &sv, uint32_t &h)
+{
+    constexpr int LB = QFmt<DT>::LANE_BYTES;
+    const u32x4 *p = (const u32x4 *)(w.qs + (cell * 64 + lane) * LB);
+    c0 = p[0];
+    if constexpr (DT == DT_Q8_0) c1 = p[1];
+    else if constexpr (DT == DT_Q6_K) {
+        const u32x2 hb = *(const u32x2 *)(w.qh + (cell * 64 + lane) * 2);
+        c1 = u32x4{hb[0], hb[1], 0u, 0u};
+    } else c1 = u32x4{0, 0, 0, 0};
+    if constexpr (is_kquant(DT)) sv = *(const u32x4 *)((const uint8_t *)w.d + (cell * 16 + col) * 16);
+    else sv = *(const u32x2 *)(w.d + cell * 64 + col * 4);
+    if constexpr (DT == DT_Q5_0) h = w.qh[cell * 64 + lane];
+    else h = 0u;
+}
+
+// fp32 factors of block bi: s0 multiplies A . codes; Q4_K adds s1 times the
+// operand's block sum (the min, plus 8 d sc for the codes' -8 bias); Q6_K
+// scales the low (s0) and high (s1) 16 values of the block separately.
+struct BlockScale {
+    float s0, s1;
+};
+
+__device__ __forceinline__ float f16lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu)); }
+__device__ __forceinline__ float f16hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+
+template <int DT>
+__device__ __forceinline__ BlockScale block_scale(const typename QScale<DT>::T &sv, int bi)
+{
+#pragma clang fp contract(off)
+    BlockScale r;
+    if constexpr (DT == DT_Q4_K) {
+        const uint32_t sm = (sv[1 + (bi >> 1)] >> (16 * (bi & 1))) & 0xFFFFu;
+        const float db = f16lo(sv[0]) * (float)(sm & 0xFFu);
+        r.s0 = db;
+        r.s1 = 8.0f * db - f16hi(sv[0]) * (float)(sm >> 8);
+    } else if constexpr (DT == DT_Q6_K) {
+        const uint32_t ss = (sv[1 + (bi >> 1)] >> (16 * (bi & 1))) & 0xFFFFu;
+        const float d = f16lo(sv[0]);
+        r.s0 = d * (float)(int8_t)(ss & 0xFFu);
+        r.s1 = d * (float)(int8_t)(ss >> 8);
+    } else {
+        const uint32_t dw = sv[bi >> 1];
+        r.s0 = (bi & 1) ? f16hi(dw) : f16lo(dw);
+        r.s1 = 0.0f;
+    }
+    return r;
+}
+
+// acc += the block's contribution for A rows xv against decoded codes wv.
+template <int DT>
+__device__ __forceinline__ void mfma_block(f32x4 &acc, const f16x8 &xv, const f16x8 &wv, const BlockScale &s)
+{
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (DT == DT_Q4_K) {
+        const f16x8 ones = {(_Float16)1, (_Float16)1, (_Float16)1, (_Float16)1,
+                            (_Float16)1, (_Float16)1, (_Float16)1, (_Float16)1};
+        const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, z, 0, 0, 0);
+        const f32x4 cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, ones, z, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(s.s1, cs[i], fmaf(s.s0, cc[i], acc[i]));
+    } else if constexpr (DT == DT_Q6_K) {
+        const _Float16 o = (_Float16)0;
+        const f16x8 wl = {wv[0], wv[1], wv[2], wv[3], o, o, o, o};
+        const f16x8 wh = {o, o, o, o, wv[4], wv[5], wv[6], wv[7]};
+        const f32x4 cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wl, z, 0, 0, 0);
+        const f32x4 ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wh, z, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(s.s1, ch[i], fmaf(s.s0, cl[i], acc[i]));
+    } else {
+        const f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, z, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(s.s0, cc[i], acc[i]);
+    }
+}
+
 // KV caches of one layer for a batch of activation vectors: vector n uses
 // slot slot_ids[n], whose K cache starts at k_base + slot*slot_stride +
 // layer_off elements (fp32 or fp16 per kv_f16); without slot_ids every

@@ -30,8 +30,33 @@ __device__ inline CellPos cell_pos(const QTensor &t, int row, int b)
 template <int DT>
 __device__ inline void block_vals8(const QTensor &t, int row, int b, int g, float val[8])
 {
+#pragma clang fp contract(off)
     constexpr int LB = QFmt<DT>::LANE_BYTES;
     const CellPos cp = cell_pos(t, row, b);
+    if constexpr (is_kquant(DT)) {
+        // the reference's arithmetic with x86 NaN rules: Q4_K
+        // (d*sc)*q - dmin*mn, Q6_K (d*scale16)*(q - 32)
+        const int lane = g * 16 + cp.col;
+        u32x4 c0, c1;
+        typename QScale<DT>::T sv;
+        uint32_t h;
+        q_load<DT>(t, cp.cell, cp.col, lane, c0, c1, sv, h);
+        const f16x8 v = deq_block<DT>(c0, c1, h, cp.bi);
+        const uint32_t pr = (sv[1 + (cp.bi >> 1)] >> (16 * (cp.bi & 1))) & 0xFFFFu;
+        if constexpr (DT == DT_Q4_K) {
+            const float db = mul_x86(f16_bits_to_f32(sv[0] & 0xFFFFu), (float)(pr & 0xFFu));
+            const float mb = mul_x86(f16_bits_to_f32(sv[0] >> 16), (float)(pr >> 8));
+#pragma unroll
+            for (int e = 0; e < 8; e++) val[e] = sub_x86(mul_x86(db, (float)v[e] + 8.0f), mb);
+        } else {
+            const float d = f16_bits_to_f32(sv[0] & 0xFFFFu);
+            const float dl = mul_x86(d, (float)(int8_t)(pr & 0xFFu));
+            const float dh = mul_x86(d, (float)(int8_t)(pr >> 8));
+#pragma unroll
+            for (int e = 0; e < 8; e++) val[e] = mul_x86(e < 4 ? dl : dh, (float)v[e]);
+        }
+        return;
+    }
     const float d = f16_bits_to_f32(t.d[cp.cell * 64 + cp.col * 4 + cp.bi]);
     const int lane = g * 16 + cp.col;
     const u32x4 *p = (const u32x4 *)(t.qs + (cp.cell * 64 + lane) * LB);

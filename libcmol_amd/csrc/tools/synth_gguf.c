@@ -15,6 +15,12 @@
  * reference quantisers (quantize_row_q8_0/q4_0/q5_0_ref): Q8_0 d=amax/127,
  * q=round(x/d); Q4_0 d=max/-8, q=min(15,(int8)(x/d+8.5)); Q5_0 d=max/-16,
  * q=min(31,(int8)(x/d+16.5)); scales rounded to fp16 (round-to-nearest-even).
+ * The K-quants use a plain min/max quantiser (not GGML's iterative search,
+ * which only changes which valid encoding a weight gets): Q4_K per 32-value
+ * sub-block scale (max - min')/15 with min' = min(0, min), super-block
+ * d = max scale / 63 and dmin = max |min'| / 63, six-bit codes of both;
+ * Q6_K per 16-value group scale max|x|/31, super-block d = max |scale| / 127,
+ * int8 group scales, codes q + 32 in 0..63.
  */
 #define _DEFAULT_SOURCE
 #include <math.h>
@@ -24,7 +30,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8 };
+enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 
 typedef struct {
     int32_t n_layers, d_model, n_heads, n_kv_heads, d_ffn, vocab, ctx_len;
@@ -169,9 +175,93 @@ static void to_q8_0(int dtype, const uint8_t *b, uint8_t *o)
     }
 }
 
+/* IEEE half -> float for finite values (the quantisers' rounded scales). */
+static float f16_value(uint16_t h)
+{
+    int e = (h >> 10) & 0x1F, m = h & 0x3FF;
+    float v = e ? ldexpf((float)(m | 0x400), e - 25) : ldexpf((float)m, -24);
+    return (h & 0x8000) ? -v : v;
+}
+
+static float f16_round(float v) { return f16_value(cmolsynth_f32_to_f16(v)); }
+
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
+
+/* Q4_K super-block of 256 values (layout src/quant.c:92-97,113-132,172-195). */
+static void q4_k_block(const float *x, uint8_t *o)
+{
+    float scale[8], mins[8], smax = 0.0f, mmax = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        float lo = 0.0f, hi = -INFINITY;
+        for (int k = 0; k < 32; k++) {
+            float v = x[32 * j + k];
+            if (v < lo) lo = v;
+            if (v > hi) hi = v;
+        }
+        scale[j] = (hi - lo) / 15.0f;
+        mins[j] = -lo;
+        if (scale[j] > smax) smax = scale[j];
+        if (mins[j] > mmax) mmax = mins[j];
+    }
+    float d = f16_round(smax / 63.0f), dmin = f16_round(mmax / 63.0f);
+    int sc[8], mn[8];
+    for (int j = 0; j < 8; j++) {
+        sc[j] = d > 0.0f ? clampi((int)lrintf(scale[j] / d), 0, 63) : 0;
+        mn[j] = dmin > 0.0f ? clampi((int)lrintf(mins[j] / dmin), 0, 63) : 0;
+    }
+    memset(o, 0, 144);
+    put16(o, cmolsynth_f32_to_f16(d));
+    put16(o + 2, cmolsynth_f32_to_f16(dmin));
+    uint8_t *s = o + 4;
+    for (int j = 0; j < 4; j++) {
+        s[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        s[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+        s[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+    }
+    for (int j = 0; j < 8; j++) {
+        float db = d * (float)sc[j], mb = dmin * (float)mn[j];
+        for (int k = 0; k < 32; k++) {
+            int q = db > 0.0f ? clampi((int)lrintf((x[32 * j + k] + mb) / db), 0, 15) : 0;
+            o[16 + 32 * (j / 2) + k] |= (uint8_t)(q << ((j & 1) ? 4 : 0));
+        }
+    }
+}
+
+/* Q6_K super-block of 256 values (layout src/quant.c:99-105,197-231). */
+static void q6_k_block(const float *x, uint8_t *o)
+{
+    float gs[16], gmax = 0.0f;
+    for (int g = 0; g < 16; g++) {
+        float a = 0.0f;
+        for (int k = 0; k < 16; k++) {
+            float v = fabsf(x[16 * g + k]);
+            if (v > a) a = v;
+        }
+        gs[g] = a / 31.0f;
+        if (gs[g] > gmax) gmax = gs[g];
+    }
+    float d = f16_round(gmax / 127.0f);
+    memset(o, 0, 210);
+    for (int g = 0; g < 16; g++) {
+        int sc = d > 0.0f ? clampi((int)lrintf(gs[g] / d), -128, 127) : 0;
+        o[192 + g] = (uint8_t)(int8_t)sc;
+        float ds = d * (float)sc;
+        for (int k = 0; k < 16; k++) {
+            int i = 16 * g + k;
+            int q = ds != 0.0f ? clampi((int)lrintf(x[i] / ds), -32, 31) : 0;
+            int u = q + 32, g8 = i / 32, j32 = i % 32;
+            o[(g8 < 4 ? 0 : 64) + (g8 & 1) * 32 + j32] |= (uint8_t)((u & 0xF) << ((g8 & 2) ? 4 : 0));
+            o[128 + (g8 < 4 ? 0 : 32) + j32] |= (uint8_t)(((u >> 4) & 3) << ((g8 & 3) * 2));
+        }
+    }
+    put16(o + 208, cmolsynth_f32_to_f16(d));
+}
+
 static size_t block_bytes(int dtype)
 {
     switch (dtype) {
+    case T_Q4_K: return 144;
+    case T_Q6_K: return 210;
     case T_Q4_0: return 18;
     case T_Q5_0: return 22;
     case T_Q8_0: return 34;
@@ -181,10 +271,12 @@ static size_t block_bytes(int dtype)
     }
 }
 
+static int block_values(int dtype) { return (dtype == T_Q4_K || dtype == T_Q6_K) ? 256 : 32; }
+
 static size_t row_bytes(int dtype, int64_t k)
 {
     if (dtype == T_F32 || dtype == T_F16) return (size_t)k * block_bytes(dtype);
-    return (size_t)(k / 32) * block_bytes(dtype);
+    return (size_t)(k / block_values(dtype)) * block_bytes(dtype);
 }
 
 /* Quantise n values (n % 32 == 0 for block formats); returns bytes written. */
@@ -197,13 +289,16 @@ int64_t cmolsynth_quantize(int dtype, const float *x, int64_t n, void *out)
         return n * 2;
     }
     size_t bb = block_bytes(dtype);
-    for (int64_t b = 0; b < n / 32; b++) {
+    const int bv = block_values(dtype);
+    if (!bb || n % bv) return -1;
+    for (int64_t b = 0; b < n / bv; b++) {
         if (dtype == T_Q8_0) q8_0_block(x + b * 32, o + b * bb);
         else if (dtype == T_Q4_0) q4_0_block(x + b * 32, o + b * bb);
         else if (dtype == T_Q5_0) q5_0_block(x + b * 32, o + b * bb);
-        else return -1;
+        else if (dtype == T_Q4_K) q4_k_block(x + b * 256, o + b * bb);
+        else q6_k_block(x + b * 256, o + b * bb);
     }
-    return (n / 32) * (int64_t)bb;
+    return (n / bv) * (int64_t)bb;
 }
 
 /* ---- tensor generation --------------------------------------------------- */

@@ -16,7 +16,7 @@ import numpy as np
 
 from . import _paths
 
-F32, F16, Q4_0, Q5_0, Q8_0 = 0, 1, 2, 6, 8
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 6, 8, 12, 14
 
 
 class _Spec(C.Structure):
@@ -202,8 +202,9 @@ def uniform_lengths(n: int, lo: int, hi: int, seed: int) -> np.ndarray:
 
 def quantize(dtype: int, x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
-    bb = {F32: 4, F16: 2, Q4_0: 18, Q5_0: 22, Q8_0: 34}[dtype]
-    nbytes = x.size * bb if dtype in (F32, F16) else x.size // 32 * bb
+    bb = {F32: 4, F16: 2, Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q6_K: 210}[dtype]
+    bv = 256 if dtype in (Q4_K, Q6_K) else 32
+    nbytes = x.size * bb if dtype in (F32, F16) else x.size // bv * bb
     out = np.empty(nbytes, np.uint8)
     if lib().cmolsynth_quantize(dtype, x.ctypes.data, x.size, out.ctypes.data) < 0:
         raise ValueError("quantize failed")

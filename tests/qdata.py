@@ -15,9 +15,16 @@ def f16bits(x):
 
 
 def random_blocks(dtype, rows, cols, seed, special=False, scale_lo=0.002, scale_hi=0.05):
-    """Raw rows of a GGUF block tensor: random codes, fp16 scales in
-    [scale_lo, scale_hi) with random sign (or the IEEE special set)."""
+    """Raw rows of a GGUF block tensor: random codes (and K-quant sub-scales),
+    fp16 scales in [scale_lo, scale_hi) with random sign (or the IEEE special
+    set)."""
     rng = np.random.default_rng(seed)
+    if dtype in (12, 14):
+        # K-quant super-block scales multiply 6-bit (Q4_K) / int8 (Q6_K)
+        # sub-scales: the same range / 64 (/ 256) gives weights of the size
+        # of the 32-value formats'
+        k = 64 if dtype == 12 else 256
+        scale_lo, scale_hi = scale_lo / k, scale_hi / k
     nb = cols // BLOCK_VALUES[dtype]
     bb = BLOCK_BYTES[dtype]
     blk = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)

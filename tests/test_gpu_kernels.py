@@ -227,3 +227,82 @@ def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens, split, 
         vref = np.ascontiguousarray(vc[i].transpose(1, 0, 2)[:L])
         want = O.attention(q[i], kref, vref, L, n_heads, n_kv, d_head)
         assert_close(got[i], want, f"attention session {i} len {L} split {split}")
+
+
+# ---- K-quants (Q4_K = 12, Q6_K = 14): super-blocks of 256 ------------------
+KQ_DEQ = [((16, 256), 1), ((37, 512), 1), ((64, 2048), 4), ((21, 1024), 8), ((5, 768), 2),
+          ((130, 2048), 1)]
+
+
+@pytest.mark.parametrize("dtype", [12, 14])
+@pytest.mark.parametrize("shape,fold", KQ_DEQ)
+def test_kquant_dequant_bit_exact(ctx, dtype, shape, fold):
+    """Every fold of the tiled K-quant layout dequantises to the reference
+    rows bit for bit."""
+    rows, cols = shape
+    raw = random_blocks(dtype, rows, cols, seed=rows * 7 + cols + dtype)
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
+    got = ctx.dequant(t)
+    want = np.stack([O.dequant_row(raw[r], cols, dtype) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [12, 14])
+def test_kquant_dequant_special_scales_bit_exact(ctx, dtype):
+    """fp16 super-block scales from the IEEE special set (zeros, subnormals,
+    max, inf, NaN payloads): the reference's x86 results, NaNs included."""
+    rows, cols = 48, 512
+    raw = random_blocks(dtype, rows, cols, seed=11 + dtype, special=True)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.dequant(t)
+    want = np.stack([O.dequant_row(raw[r], cols, dtype) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [12, 14])
+def test_kquant_upload_concat_interleave_chunked(ctx, dtype):
+    cols = 512
+    a, b, c = (random_blocks(dtype, r, cols, seed=s) for r, s in ((40, 1), (24, 2), (24, 3)))
+    bb = a.shape[1]
+    t = ctx.qtensor([a, b, c], dtype, cols, [40, 24, 24], mode=0, staging_bytes=bb * 5, fold=4)
+    want = np.concatenate([a, b, c])
+    ref = np.stack([O.dequant_row(want[r], cols, dtype) for r in range(want.shape[0])])
+    assert np.array_equal(ctx.dequant(t).view(np.uint32), ref.view(np.uint32))
+    t2 = ctx.qtensor([b, c], dtype, cols, [24, 24], mode=1, staging_bytes=bb * 7)
+    il = np.empty((48, bb), np.uint8)
+    il[0::2], il[1::2] = b, c
+    ref2 = np.stack([O.dequant_row(il[r], cols, dtype) for r in range(48)])
+    assert np.array_equal(ctx.dequant(t2).view(np.uint32), ref2.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [12, 14])
+@pytest.mark.parametrize("rows,cols,fold,n", [
+    (64, 256, 1, 1), (2048, 2048, 4, 1), (3072, 2048, 4, 1), (11008, 2048, 1, 1), (2048, 11008, 4, 1),
+    (300, 1024, 8, 1), (96, 768, 2, 1), (256, 2048, 1, 3), (512, 2048, 4, 2), (256, 2048, 1, 8),
+    (300, 2048, 1, 17), (2048, 11008, 1, 32), (384, 2048, 1, 40), (2048, 11008, 4, 65),
+    (300, 2048, 1, 130)])
+def test_kquant_gemv_gemm_match_oracle(ctx, dtype, rows, cols, fold, n):
+    """Q4_K / Q6_K through the matvec (n <= 8), the vector-group kernel
+    (9..32) and the tiled GEMM (> 32), folded and unfolded, against the
+    oracle in the reference's AVX-512 order."""
+    raw = random_blocks(dtype, rows, cols, seed=rows * 5 + cols + n + dtype)
+    x = np.random.default_rng(n + dtype).standard_normal((n, cols)).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
+    got = ctx.gemm(t, x)
+    want = O.matmul(raw, np.ascontiguousarray(x.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"q{dtype} {rows}x{cols} fold {fold} n {n}")
+
+
+@pytest.mark.parametrize("dtype", [12, 14])
+@pytest.mark.parametrize("n", [1, 20, 64])
+def test_kquant_rmsnorm_prologue(ctx, dtype, n):
+    rows, cols = 512, 2048
+    raw = random_blocks(dtype, rows, cols, seed=9 + n)
+    rng = np.random.default_rng(11 + n)
+    x = (rng.standard_normal((n, cols)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows])
+    got = ctx.gemm(t, x, norm_w=w, eps=1e-6)
+    xn = np.stack([O.rms_norm(xi, w, 1e-6) for xi in x])
+    want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"q{dtype} rmsnorm n {n}")
