@@ -110,6 +110,10 @@ PRESETS = {
     "small-q5_0": ModelSpec(3, 320, 5, 1, 640, 1024, ctx_len=4096, wtype=Q5_0, embd_type=Q5_0),
     "small-q8_0-untied": ModelSpec(2, 192, 3, 3, 512, 1024, ctx_len=1024, wtype=Q8_0,
                                    embd_type=Q8_0, out_type=Q8_0),
+    # K-quant layers (every matrix dimension a multiple of 256)
+    "small-q4_k": ModelSpec(3, 256, 4, 2, 768, 1024, ctx_len=4096, wtype=Q4_K, embd_type=Q6_K),
+    "small-q6_k-untied": ModelSpec(2, 512, 8, 2, 1536, 1024, ctx_len=1024, wtype=Q6_K,
+                                   embd_type=Q4_K, out_type=Q6_K),
 }
 
 _lib = None

@@ -43,7 +43,8 @@ def test_matches_reference_golden(gpu, model_dir, name):
 
 
 @pytest.mark.parametrize("preset", ["micro-q8_0", "micro-q4_0", "micro-q5_0", "small-q4_0",
-                                    "small-q5_0", "small-q8_0-untied"])
+                                    "small-q5_0", "small-q8_0-untied", "small-q4_k",
+                                    "small-q6_k-untied"])
 def test_greedy_tokens_match_oracle(gpu, model_dir, preset):
     spec = synth.PRESETS[preset].replace(wstd=0.08)
     path = synth.model_file(spec, model_dir)
@@ -58,7 +59,23 @@ def test_greedy_tokens_match_oracle(gpu, model_dir, preset):
     m.close()
 
 
-@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "small-q8_0-untied"])
+@pytest.mark.parametrize("preset", ["small-q4_k", "small-q6_k-untied"])
+def test_kquant_models_match_reference(gpu, model_dir, preset):
+    """Q4_K / Q6_K models: the greedy ids the built reference produced
+    (tests/golden/make_kquant_golden.py), through the prompt GEMM and the
+    decode graph."""
+    kq = np.load(os.path.join(os.path.dirname(__file__), "golden", "kquant.npz"))
+    spec = synth.PRESETS[preset].replace(wstd=0.08)
+    path = synth.model_file(spec, model_dir)
+    m = native.Model(path, max_ctx=128, max_sessions=1)
+    s = m.acquire()
+    got = s.generate_ids(kq[f"model_{preset}_prompt"], native.greedy_params(48), 48)
+    assert got.tolist() == kq[f"model_{preset}_ids"].tolist()
+    m.close()
+
+
+@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "small-q8_0-untied", "small-q4_k",
+                                    "small-q6_k-untied"])
 def test_forward_logits_match_oracle(gpu, model_dir, preset):
     spec = synth.PRESETS[preset]
     path = synth.model_file(spec, model_dir)
@@ -122,7 +139,7 @@ def test_smollm2_135m_greedy_128(gpu, model_dir):
     m.close()
 
 
-@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "micro-q8_0"])
+@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "micro-q8_0", "small-q4_k"])
 def test_decode_batch_matches_oracle(gpu, model_dir, preset):
     """Lock-step decode of several sessions with ragged prompt lengths (one
     launch per stage for all of them) continues every session exactly as the
@@ -176,7 +193,7 @@ def test_decode_batch_matches_single_session_steps(gpu, model_dir, preset, sessi
 
 
 @pytest.mark.parametrize("preset,chunk", [("small-q4_0", 16), ("small-q5_0", 7), ("small-q8_0-untied", 64),
-                                          ("micro-q4_0", 5)])
+                                          ("micro-q4_0", 5), ("small-q4_k", 16), ("small-q6_k-untied", 40)])
 def test_chunked_prefill_matches_oracle(gpu, model_dir, preset, chunk):
     """A prompt longer than prefill_chunk runs as several batched passes (the
     later ones attend to the cache the earlier ones wrote): logits after the

@@ -127,6 +127,18 @@ def test_kquant_matmul_matches_reference_orders(name, dt, shape):
         assert np.array_equal(bits(O.matmul(a, b, m, k, dt, order)), KQ[key + suffix]), suffix
 
 
+@pytest.mark.parametrize("preset", ["small-q4_k", "small-q6_k-untied"])
+def test_kquant_models_match_reference(preset, model_dir):
+    """Whole models with Q4_K / Q6_K layers (and K-quant embedding / LM
+    head): the oracle's greedy continuation equals the reference's."""
+    spec = synth.PRESETS[preset].replace(wstd=0.08)
+    path = synth.model_file(spec, model_dir)
+    prompt = KQ[f"model_{preset}_prompt"]
+    assert np.array_equal(prompt, synth.tokens(16, 42, spec.vocab))
+    got = O.Model(path, 128).generate(prompt, 48)
+    assert got.tolist() == KQ[f"model_{preset}_ids"].tolist()
+
+
 def test_q4_k_closed_form():
     """Q4_K: sub-block j of a super-block with d = 1, dmin = 0.5, scale
     j + 1 and min 2j (the six-bit packing spelled out by hand, bits 4-5 of
