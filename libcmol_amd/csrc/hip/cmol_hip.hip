@@ -448,7 +448,11 @@ int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kca
 namespace {
 
 struct MLayer {
-    cmolhip_qtensor_t qkv{}, o{}, gu{}, down{};
+    // q|k|v rows in runs of parts that share a format (one tensor per run;
+    // a single run unless the GGUF mixes formats, e.g. a Q6_K attn_v)
+    cmolhip_qtensor_t qkv[3]{};
+    int qkv_row0[3]{}, n_qkv = 1;
+    cmolhip_qtensor_t o{}, gu{}, down{};
     float *attn_norm = nullptr, *ffn_norm = nullptr;
     int rope_on = 1;
 };
@@ -519,6 +523,26 @@ int pick_split(int max_ctx)
 
 bool is_block_fmt(int dt) { return dt == DT_Q4_0 || dt == DT_Q5_0 || dt == DT_Q8_0 || is_kquant(dt); }
 
+// Runs of consecutive q / k / v parts that share a format: run r covers
+// parts first[r] .. first[r] + count[r] - 1 (rows of q, k, v: d, kvd, kvd).
+int qkv_runs(const cmolhip_layer_tensors_t &L, int first[3], int count[3])
+{
+    const int dt[3] = {L.q.dtype, L.k.dtype, L.v.dtype};
+    int n = 0;
+    for (int p = 0; p < 3; p++) {
+        if (n && dt[p] == dt[first[n - 1]]) {
+            count[n - 1]++;
+        } else {
+            first[n] = p;
+            count[n] = 1;
+            n++;
+        }
+    }
+    return n;
+}
+
+int qkv_part_rows(const cmolhip_hparams_t &h, int p) { return p == 0 ? h.d_model : h.n_kv_heads * h.d_head; }
+
 // Byte sizes of everything the model puts in the arena, in creation order.
 struct Plan {
     std::vector<size_t> sizes;
@@ -586,7 +610,9 @@ int persist_format(const cmolhip_model_desc_t *d)
     if (dt != DT_Q4_0 && dt != DT_Q5_0 && dt != DT_Q8_0) return 0;   // no K-quant kernel
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &L = d->layers[l];
-        if (L.q.dtype != dt || L.o.dtype != dt || L.gate.dtype != dt || L.down.dtype != dt) return 0;
+        if (L.q.dtype != dt || L.k.dtype != dt || L.v.dtype != dt || L.o.dtype != dt ||
+            L.gate.dtype != dt || L.down.dtype != dt)
+            return 0;
     }
     return dt;
 }
@@ -639,7 +665,10 @@ int validate_desc(const cmolhip_model_desc_t *d)
             !chk(L.gate, h.d_ffn, h.d_model) || !chk(L.up, h.d_ffn, h.d_model) ||
             !chk(L.down, h.d_model, h.d_ffn))
             return E_UNSUPPORTED;
-        if (L.q.dtype != L.k.dtype || L.q.dtype != L.v.dtype || L.gate.dtype != L.up.dtype)
+        // q, k and v may differ in format but share one activation operand,
+        // whose k order differs for Q8_0; gate and up are interleaved rows
+        const bool q8 = L.q.dtype == DT_Q8_0;
+        if (q8 != (L.k.dtype == DT_Q8_0) || q8 != (L.v.dtype == DT_Q8_0) || L.gate.dtype != L.up.dtype)
             return E_UNSUPPORTED;
         if (!chk_norm(L.attn_norm, h.d_model) || !chk_norm(L.ffn_norm, h.d_model)) return E_INVALID;
         if (L.q_norm.data || L.k_norm.data) return E_UNSUPPORTED;
@@ -783,7 +812,6 @@ void plan_persist(Plan &P, const cmolhip_hparams_t &h)
 Plan make_plan(const cmolhip_model_desc_t *d)
 {
     const cmolhip_hparams_t &h = d->hp;
-    const int kvd = h.n_kv_heads * h.d_head;
     const int ms = attn_max_splits(h.max_ctx, pick_split(h.max_ctx));
     Plan P;
     size_t big = 0;
@@ -801,7 +829,14 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(P.staging);
     for (int l = 0; l < h.n_layers; l++) {
         const auto &L = d->layers[l];
-        add_q(P, L.q.dtype, h.d_model + 2 * kvd, h.d_model, layer_fold(d, h.d_model + 2 * kvd, h.d_model));
+        int first[3], count[3];
+        const int nr = qkv_runs(L, first, count);
+        for (int r = 0; r < nr; r++) {
+            int rows = 0;
+            for (int p = first[r]; p < first[r] + count[r]; p++) rows += qkv_part_rows(h, p);
+            const int dt = r == 0 ? L.q.dtype : first[r] == 1 ? L.k.dtype : L.v.dtype;
+            add_q(P, dt, rows, h.d_model, layer_fold(d, rows, h.d_model));
+        }
         add_q(P, L.o.dtype, h.d_model, h.d_model, layer_fold(d, h.d_model, h.d_model));
         add_q(P, L.gate.dtype, 2 * h.d_ffn, h.d_model, layer_fold(d, 2 * h.d_ffn, h.d_model));
         add_q(P, L.down.dtype, h.d_model, h.d_ffn, layer_fold(d, h.d_model, h.d_ffn));
@@ -899,13 +934,12 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
     const int d = hp.d_model, kvd = hp.n_kv_heads * hp.d_head, P = d;
     const float eps = hp.rms_eps;
     RC(launch_embed(to_qt(m->embd), B.steps, 3, B.x, d,
-                    act_out(B.op_qkv, m->layers[0].qkv.dtype, n, m->layers[0].attn_norm, B.ss_a, P),
+                    act_out(B.op_qkv, m->layers[0].qkv[0].dtype, n, m->layers[0].attn_norm, B.ss_a, P),
                     B.argmax, n, st));
     int ss_count = d / 32;   // the embedding writes one partial per 32 inputs
     for (int l = 0; l < hp.n_layers; l++) {
         const MLayer &L = m->layers[l];
         GemvArgs g{};
-        g.w = to_qt(L.qkv);
         g.in = act_in(B.op_qkv, n, B.ss_a, ss_count, P, eps);
         g.out = B.q;
         g.out_stride = d;
@@ -921,7 +955,11 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         g.pos = B.steps + 1;
         g.pos_stride = 3;
         g.part = B.part;
-        RC(launch_gemv(g, EPI_QKV, st));
+        for (int r = 0; r < L.n_qkv; r++) {   // one launch per run of q|k|v formats
+            g.w = to_qt(L.qkv[r]);
+            g.row_base = L.qkv_row0[r];
+            RC(launch_gemv(g, EPI_QKV, st));
+        }
 
         AttnArgs at{};
         at.q = B.q;
@@ -970,7 +1008,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         gd.out_stride = d;
         gd.n = n;
         if (l + 1 < hp.n_layers)
-            gd.next = act_out(B.op_qkv, m->layers[l + 1].qkv.dtype, n, m->layers[l + 1].attn_norm, B.ss_a, P);
+            gd.next = act_out(B.op_qkv, m->layers[l + 1].qkv[0].dtype, n, m->layers[l + 1].attn_norm, B.ss_a, P);
         else
             gd.next = act_out(B.op_lm, lm_tensor(m).dtype, n, m->out_norm, B.ss_a, P);
         gd.part = B.part;
@@ -1005,7 +1043,7 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
     kv.slot_stride = m->slot_stride;
     kv.slot_ids = F.slot_ids;
     RC(launch_embed(to_qt(m->embd), F.steps, 3, F.x, d,
-                    act_out(F.op_qkv, m->layers[0].qkv.dtype, n, m->layers[0].attn_norm, F.ss_a, P),
+                    act_out(F.op_qkv, m->layers[0].qkv[0].dtype, n, m->layers[0].attn_norm, F.ss_a, P),
                     nullptr, n, st));
     int ss_count = d / 32;
     const int tile_count = (d + 15) / 16;   // GEMM residual partials: one per 16 rows
@@ -1013,7 +1051,6 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         const MLayer &L = m->layers[l];
         kv.layer_off = (size_t)l * m->layer_stride;
         GemvArgs g{};
-        g.w = to_qt(L.qkv);
         g.in = act_in(F.op_qkv, n, F.ss_a, ss_count, P, eps);
         g.out = F.q;
         g.out_stride = d;
@@ -1028,7 +1065,11 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         g.kv = kv;
         g.pos = F.steps + 1;
         g.pos_stride = 3;
-        RC(launch_gemm(g, EPI_QKV, st));
+        for (int r = 0; r < L.n_qkv; r++) {
+            g.w = to_qt(L.qkv[r]);
+            g.row_base = L.qkv_row0[r];
+            RC(launch_gemm(g, EPI_QKV, st));
+        }
 
         AttnArgs at{};
         at.q = F.q;
@@ -1075,7 +1116,7 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         gd.out_stride = d;
         gd.n = n;
         if (l + 1 < hp.n_layers)
-            gd.next = act_out(F.op_qkv, m->layers[l + 1].qkv.dtype, n, m->layers[l + 1].attn_norm, F.ss_a, P);
+            gd.next = act_out(F.op_qkv, m->layers[l + 1].qkv[0].dtype, n, m->layers[l + 1].attn_norm, F.ss_a, P);
         else
             gd.next = act_out(F.op_lm, lm_tensor(m).dtype, n, m->out_norm, F.ss_a, P);
         RC(launch_gemm(gd, EPI_RESID, st));
@@ -1209,11 +1250,11 @@ int build_persist(cmolhip_model *m, int dt)
     for (int l = 0; l < h.n_layers; l++) {
         const MLayer &L = m->layers[l];
         PkLayer &Y = ly[l];
-        Y.qkv = to_qt(L.qkv);
+        Y.qkv = to_qt(L.qkv[0]);   // one run: the persistent kernel needs uniform formats
         Y.o = to_qt(L.o);
         Y.gu = to_qt(L.gu);
         Y.down = to_qt(L.down);
-        need(L.qkv);
+        need(L.qkv[0]);
         need(L.o);
         need(L.gu);
         need(L.down);
@@ -1322,10 +1363,17 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &T = d->layers[l];
         MLayer &L = m->layers[l];
-        const int kvd = h.n_kv_heads * h.d_head;
         const cmolhip_host_tensor_t *qkv[3] = {&T.q, &T.k, &T.v};
-        RC(upload_q(c, 3, qkv, CMOLHIP_PARTS_CONCAT, layer_fold(d, h.d_model + 2 * kvd, h.d_model),
-                    stg, P.staging, &L.qkv));
+        int first[3], count[3];
+        L.n_qkv = qkv_runs(T, first, count);
+        for (int r = 0, row0 = 0; r < L.n_qkv; r++) {
+            int rows = 0;
+            for (int p = first[r]; p < first[r] + count[r]; p++) rows += qkv_part_rows(h, p);
+            L.qkv_row0[r] = row0;
+            RC(upload_q(c, count[r], qkv + first[r], CMOLHIP_PARTS_CONCAT, layer_fold(d, rows, h.d_model),
+                        stg, P.staging, &L.qkv[r]));
+            row0 += rows;
+        }
         const cmolhip_host_tensor_t *o[1] = {&T.o};
         RC(upload_q(c, 1, o, CMOLHIP_PARTS_CONCAT, layer_fold(d, h.d_model, h.d_model), stg,
                     P.staging, &L.o));

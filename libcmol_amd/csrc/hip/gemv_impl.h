@@ -195,7 +195,7 @@ __device__ __forceinline__ void epi_pre_cs(const GemvArgs &a, int epi, int row, 
         const int pos = a.pos ? p.pos : a.pos0;
         p.pos = min(max(pos, 0), a.max_ctx - 1);
         p.kvo = (a.kv.slot_ids ? (size_t)p.slot * a.kv.slot_stride : 0) + a.kv.layer_off;
-        p.cs = rope_cs(a, row, p.pos);
+        p.cs = rope_cs(a, row + a.row_base, p.pos);
     }
 }
 
@@ -239,11 +239,12 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
     } else if constexpr (EPI == EPI_QKV) {
         const float partner = __shfl_xor(y, 1, 64);
         if (act) {
+            const int grow = row + a.row_base;
             if (has_pre) {
-                qkv_out<M>(a, v, row, y, partner, pre.cs, pre.pos, pre.kvo);
+                qkv_out<M>(a, v, grow, y, partner, pre.cs, pre.pos, pre.kvo);
             } else {
                 const int pos = epi_pos(a, v);
-                qkv_out<M>(a, v, row, y, partner, rope_cs(a, row, pos), pos, kv_offset(a.kv, v));
+                qkv_out<M>(a, v, grow, y, partner, rope_cs(a, grow, pos), pos, kv_offset(a.kv, v));
             }
         }
     } else if constexpr (EPI == EPI_LOGITS) {

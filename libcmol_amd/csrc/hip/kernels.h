@@ -225,8 +225,9 @@ struct GemvArgs {
     const float *res;       // EPI_RESID: residual input [n][out_stride] (nullptr: out itself)
     int n;                  // activation vectors
     ActOut next;            // EPI_RESID / EPI_SWIGLU: operand of the consumer
-    // EPI_QKV
-    int nq, nkv, d_head, max_ctx, kv_f16, rope_on;
+    // EPI_QKV (row_base: first output row of this launch in the q|k|v rows,
+    // when the three are split over tensors of different formats)
+    int nq, nkv, d_head, max_ctx, kv_f16, rope_on, row_base;
     const float *rope;      // [max_ctx][d_head/2][2]
     KVRef kv;
     const int32_t *pos;     // per-vector position, pos[n * pos_stride] (nullptr: pos0)

@@ -36,6 +36,7 @@ typedef struct {
     int32_t n_layers, d_model, n_heads, n_kv_heads, d_ffn, vocab, ctx_len;
     int32_t wtype, embd_type, out_type;   /* out_type < 0: tied embeddings */
     int32_t nope_interval, eos_id, qk_norm, arch_smollm3, transcode_q8;
+    int32_t v_type, down_type;            /* attn_v / ffn_down format (< 0: wtype) */
     float rope_base, rms_eps, wstd, norm_jitter;
     uint64_t seed;
 } cmolsynth_spec_t;
@@ -432,7 +433,7 @@ static int write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads,
         snprintf(nm, sizeof nm, "blk.%d.attn_norm.weight", l);   ADD(nm, T_F32, d, 1, 1);
         snprintf(nm, sizeof nm, "blk.%d.attn_q.weight", l);      ADD(nm, s->wtype, d, d, 0);
         snprintf(nm, sizeof nm, "blk.%d.attn_k.weight", l);      ADD(nm, s->wtype, d, kvd, 0);
-        snprintf(nm, sizeof nm, "blk.%d.attn_v.weight", l);      ADD(nm, s->wtype, d, kvd, 0);
+        snprintf(nm, sizeof nm, "blk.%d.attn_v.weight", l);      ADD(nm, s->v_type >= 0 ? s->v_type : s->wtype, d, kvd, 0);
         snprintf(nm, sizeof nm, "blk.%d.attn_output.weight", l); ADD(nm, s->wtype, d, d, 0);
         if (s->qk_norm) {
             snprintf(nm, sizeof nm, "blk.%d.attn_q_norm.weight", l); ADD(nm, T_F32, dh, 1, 1);
@@ -441,7 +442,7 @@ static int write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads,
         snprintf(nm, sizeof nm, "blk.%d.ffn_norm.weight", l);    ADD(nm, T_F32, d, 1, 1);
         snprintf(nm, sizeof nm, "blk.%d.ffn_gate.weight", l);    ADD(nm, s->wtype, d, s->d_ffn, 0);
         snprintf(nm, sizeof nm, "blk.%d.ffn_up.weight", l);      ADD(nm, s->wtype, d, s->d_ffn, 0);
-        snprintf(nm, sizeof nm, "blk.%d.ffn_down.weight", l);    ADD(nm, s->wtype, s->d_ffn, d, 0);
+        snprintf(nm, sizeof nm, "blk.%d.ffn_down.weight", l);    ADD(nm, s->down_type >= 0 ? s->down_type : s->wtype, s->d_ffn, d, 0);
     }
     ADD("output_norm.weight", T_F32, d, 1, 1);
     if (s->out_type >= 0) ADD("output.weight", s->out_type, d, s->vocab, 0);

@@ -23,7 +23,7 @@ class _Spec(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_layers", "d_model", "n_heads", "n_kv_heads", "d_ffn", "vocab", "ctx_len",
         "wtype", "embd_type", "out_type", "nope_interval", "eos_id", "qk_norm",
-        "arch_smollm3", "transcode_q8")] + [
+        "arch_smollm3", "transcode_q8", "v_type", "down_type")] + [
         ("rope_base", C.c_float), ("rms_eps", C.c_float), ("wstd", C.c_float),
         ("norm_jitter", C.c_float), ("seed", C.c_uint64)]
 
@@ -66,6 +66,8 @@ class ModelSpec:
     qk_norm: int = 0
     arch_smollm3: int = 0
     transcode_q8: int = 0         # write Q4_0/Q5_0 tensors as lossless Q8_0
+    v_type: int = -1              # attn_v format (-1: wtype)
+    down_type: int = -1           # ffn_down format (-1: wtype)
     rope_base: float = 10000.0
     rms_eps: float = 1e-5
     wstd: float = 0.02
@@ -114,6 +116,9 @@ PRESETS = {
     "small-q4_k": ModelSpec(3, 256, 4, 2, 768, 1024, ctx_len=4096, wtype=Q4_K, embd_type=Q6_K),
     "small-q6_k-untied": ModelSpec(2, 512, 8, 2, 1536, 1024, ctx_len=1024, wtype=Q6_K,
                                    embd_type=Q4_K, out_type=Q6_K),
+    # the Q4_K_M mix: Q4_K projections, Q6_K attn_v / ffn_down / embedding
+    "small-q4_k_m": ModelSpec(3, 512, 8, 2, 1536, 1024, ctx_len=4096, wtype=Q4_K, embd_type=Q6_K,
+                              v_type=Q6_K, down_type=Q6_K),
 }
 
 _lib = None

@@ -29,7 +29,7 @@ from tests.qdata import random_blocks  # noqa: E402
 KTYPES = {"q4_k": 12, "q6_k": 14}
 DEQ_SHAPE = (8, 1024)
 MM_SHAPES = [(16, 512, 1), (24, 768, 3)]
-MODEL_PRESETS = ["small-q4_k", "small-q6_k-untied"]
+MODEL_PRESETS = ["small-q4_k", "small-q6_k-untied", "small-q4_k_m"]
 
 
 def main():

@@ -44,7 +44,7 @@ def test_matches_reference_golden(gpu, model_dir, name):
 
 @pytest.mark.parametrize("preset", ["micro-q8_0", "micro-q4_0", "micro-q5_0", "small-q4_0",
                                     "small-q5_0", "small-q8_0-untied", "small-q4_k",
-                                    "small-q6_k-untied"])
+                                    "small-q6_k-untied", "small-q4_k_m"])
 def test_greedy_tokens_match_oracle(gpu, model_dir, preset):
     spec = synth.PRESETS[preset].replace(wstd=0.08)
     path = synth.model_file(spec, model_dir)
@@ -59,7 +59,7 @@ def test_greedy_tokens_match_oracle(gpu, model_dir, preset):
     m.close()
 
 
-@pytest.mark.parametrize("preset", ["small-q4_k", "small-q6_k-untied"])
+@pytest.mark.parametrize("preset", ["small-q4_k", "small-q6_k-untied", "small-q4_k_m"])
 def test_kquant_models_match_reference(gpu, model_dir, preset):
     """Q4_K / Q6_K models: the greedy ids the built reference produced
     (tests/golden/make_kquant_golden.py), through the prompt GEMM and the
@@ -75,7 +75,7 @@ def test_kquant_models_match_reference(gpu, model_dir, preset):
 
 
 @pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "small-q8_0-untied", "small-q4_k",
-                                    "small-q6_k-untied"])
+                                    "small-q6_k-untied", "small-q4_k_m"])
 def test_forward_logits_match_oracle(gpu, model_dir, preset):
     spec = synth.PRESETS[preset]
     path = synth.model_file(spec, model_dir)
@@ -139,7 +139,7 @@ def test_smollm2_135m_greedy_128(gpu, model_dir):
     m.close()
 
 
-@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "micro-q8_0", "small-q4_k"])
+@pytest.mark.parametrize("preset", ["small-q4_0", "small-q5_0", "micro-q8_0", "small-q4_k", "small-q4_k_m"])
 def test_decode_batch_matches_oracle(gpu, model_dir, preset):
     """Lock-step decode of several sessions with ragged prompt lengths (one
     launch per stage for all of them) continues every session exactly as the
@@ -193,7 +193,8 @@ def test_decode_batch_matches_single_session_steps(gpu, model_dir, preset, sessi
 
 
 @pytest.mark.parametrize("preset,chunk", [("small-q4_0", 16), ("small-q5_0", 7), ("small-q8_0-untied", 64),
-                                          ("micro-q4_0", 5), ("small-q4_k", 16), ("small-q6_k-untied", 40)])
+                                          ("micro-q4_0", 5), ("small-q4_k", 16), ("small-q6_k-untied", 40),
+                                          ("small-q4_k_m", 45)])
 def test_chunked_prefill_matches_oracle(gpu, model_dir, preset, chunk):
     """A prompt longer than prefill_chunk runs as several batched passes (the
     later ones attend to the cache the earlier ones wrote): logits after the
@@ -223,3 +224,20 @@ def test_chunked_prefill_matches_oracle(gpu, model_dir, preset, chunk):
     om2 = O.Model(path, 64)
     assert got.tolist() == om2.generate(prompt, 12).tolist()
     m.close()
+
+
+def test_mixed_qkv_formats(gpu, model_dir):
+    """q / k / v of different formats run as separate launches over one
+    operand: a Q5_0 attn_v next to Q4_0 q / k matches the oracle; a Q8_0
+    attn_v (another operand order) is refused at load."""
+    spec = synth.PRESETS["small-q4_0"].replace(wstd=0.08, v_type=synth.Q5_0)
+    path = synth.model_file(spec, model_dir)
+    prompt = synth.tokens(16, 42, spec.vocab)
+    m = native.Model(path, max_ctx=96, max_sessions=1)
+    s = m.acquire()
+    got = s.generate_ids(prompt, native.greedy_params(32), 32)
+    m.close()
+    assert got.tolist() == O.Model(path, 96).generate(prompt, 32).tolist()
+    bad = synth.model_file(synth.PRESETS["small-q4_0"].replace(v_type=synth.Q8_0), model_dir)
+    with pytest.raises(RuntimeError, match=str(native.CMOL_ERR_UNSUPPORTED)):
+        native.Model(bad, max_ctx=64, max_sessions=1)

@@ -127,7 +127,7 @@ def test_kquant_matmul_matches_reference_orders(name, dt, shape):
         assert np.array_equal(bits(O.matmul(a, b, m, k, dt, order)), KQ[key + suffix]), suffix
 
 
-@pytest.mark.parametrize("preset", ["small-q4_k", "small-q6_k-untied"])
+@pytest.mark.parametrize("preset", ["small-q4_k", "small-q6_k-untied", "small-q4_k_m"])
 def test_kquant_models_match_reference(preset, model_dir):
     """Whole models with Q4_K / Q6_K layers (and K-quant embedding / LM
     head): the oracle's greedy continuation equals the reference's."""
