@@ -40,15 +40,23 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def q4_bytes(m, k, n):
-    """Algorithmic HBM bytes of one Q4_0 matvec launch: the weight blocks
-    (18 bytes per 32 weights), the activation operand (an f16 high and an f16
-    low part per input and vector) and the fp32 outputs."""
-    return m * (k // 32) * 18 + 4 * k * n + 4 * m * n
+BLOCK = {synth.Q4_0: (32, 18), synth.Q5_0: (32, 22), synth.Q8_0: (32, 34),
+         synth.Q4_K: (256, 144), synth.Q6_K: (256, 210)}
+DT_NAME = {synth.Q4_0: "Q4_0", synth.Q5_0: "Q5_0", synth.Q8_0: "Q8_0", synth.Q4_K: "Q4_K",
+           synth.Q6_K: "Q6_K"}
 
 
-def bench_matvec(rows, cols, n, copies, launches, fold=None):
-    """Average duration of the Q4_0 matvec kernel over `copies` distinct
+def q4_bytes(m, k, n, dtype=synth.Q4_0):
+    """Algorithmic HBM bytes of one matvec launch: the weight blocks in their
+    GGUF size (Q4_0: 18 bytes per 32 weights; Q4_K 144 / Q6_K 210 per 256),
+    the activation operand (an f16 high and an f16 low part per input and
+    vector) and the fp32 outputs."""
+    bv, bb = BLOCK[dtype]
+    return m * (k // bv) * bb + 4 * k * n + 4 * m * n
+
+
+def bench_matvec(rows, cols, n, copies, launches, fold=None, dtype=synth.Q4_0):
+    """Average duration of the matvec kernel (Q4_0 unless `dtype`) over `copies` distinct
     weight buffers (defeating the 256 MB Infinity Cache): every launch records
     a pair of HIP events at the kernel's own start and end (on the stream it
     runs on).  The weights use the fold a model serving n sessions gives this
@@ -57,13 +65,13 @@ def bench_matvec(rows, cols, n, copies, launches, fold=None):
     if fold is None:
         fold = native.lib().cmolhip_pick_fold(rows, cols, n)
     w = synth.normal(rows * cols, seed=1234, stream=rows * 7 + cols, std=0.02)
-    raw = synth.quantize(synth.Q4_0, w).reshape(rows, -1)
-    tensor_bytes = native.lib().cmolhip_qtensor_bytes(2, rows, cols, fold)
+    raw = synth.quantize(dtype, w).reshape(rows, -1)
+    tensor_bytes = native.lib().cmolhip_qtensor_bytes(dtype, rows, cols, fold)
     arena = (copies * (tensor_bytes + 4096) + raw.nbytes + n * cols * 4 + n * rows * 4
              + native.lib().cmolhip_act_bytes(cols, n) + (64 << 20))
     ctx = native.Ctx(arena)
     stg = ctx.alloc(raw.nbytes)
-    ts = [ctx.qtensor([raw], 2, cols, [rows], staging_bytes=raw.nbytes, staging=stg, fold=fold)
+    ts = [ctx.qtensor([raw], dtype, cols, [rows], staging_bytes=raw.nbytes, staging=stg, fold=fold)
           for _ in range(copies)]
     x = np.random.default_rng(1).standard_normal((n, cols)).astype(np.float32)
     dx = ctx.upload(x)
@@ -88,9 +96,10 @@ def bench_matvec(rows, cols, n, copies, launches, fold=None):
     for ev in evs:
         ev.close()
     ctx.close()
-    b = q4_bytes(rows, cols, n)
+    b = q4_bytes(rows, cols, n, dtype)
     flops = 2.0 * rows * cols * n
-    out = {"shape": f"{rows}x{cols}", "n": n, "fold": fold, "us_per_launch": per_launch_s * 1e6,
+    out = {"shape": f"{rows}x{cols}", "dtype": DT_NAME[dtype], "n": n, "fold": fold,
+           "us_per_launch": per_launch_s * 1e6,
            "bytes_per_launch": b, "GBps": b / per_launch_s / 1e9,
            "frac_of_peak": b / per_launch_s / 1e9 / HBM_PEAK_GBPS}
     if n > 32:
@@ -257,6 +266,12 @@ def main():
         for rows, cols in ((11008, 2048), (2048, 11008)):
             for n in (1, 8, 32):
                 r = bench_matvec(rows, cols, n, copies=64, launches=256)
+                log(json.dumps(r))
+                mv.append(r)
+        # the K-quant formats of Q4_K_M files on the same shapes, one vector
+        for dt in (synth.Q4_K, synth.Q6_K):
+            for rows, cols in ((11008, 2048), (2048, 11008)):
+                r = bench_matvec(rows, cols, 1, copies=64, launches=256, dtype=dt)
                 log(json.dumps(r))
                 mv.append(r)
     gm = []
