@@ -214,6 +214,83 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     }
 }
 
+// One wave per (head of q|k|v, vector): lane l holds dims DL*l .. DL*l+DL-1
+// (DL = d_head/64; d_head 16/32 use the first d_head lanes).  q and k heads:
+// RMSNorm s = 1/sqrtf(sum x^2 / d_head + eps), y = w * (x * s) (the
+// reference's cmol_rms_norm order, wave-order sum), then RoPE on the pairs
+// (2i, 2i+1) with the QKV epilogue's arithmetic; then q -> a.q, k and v ->
+// the cache at the vector's position.
+template <int DL>
+__global__ __launch_bounds__(64) void k_qk_rope(QkArgs a)
+{
+#pragma clang fp contract(off)
+    const int hh = blockIdx.x, v = blockIdx.y, lane = threadIdx.x;
+    const int dh = a.d_head;
+    const bool isq = hh < a.n_heads, isk = !isq && hh < a.n_heads + a.n_kv;
+    const int row0 = hh * dh;   // q rows, then k rows, then v rows
+    const bool act = lane * DL < dh;
+    const float *src = a.raw + (size_t)v * a.raw_stride + row0;
+    float x[DL];
+#pragma unroll
+    for (int j = 0; j < DL; j++) x[j] = act ? src[lane * DL + j] : 0.0f;
+    const float *w = isq ? a.qn_w : isk ? a.kn_w : nullptr;
+    if (w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DL; j++) ss += x[j] * x[j];
+        ss = wave_sum(ss);
+        const float sc = 1.0f / sqrtf(ss / (float)dh + a.eps);
+#pragma unroll
+        for (int j = 0; j < DL; j++) x[j] = act ? w[lane * DL + j] * (x[j] * sc) : 0.0f;
+    }
+    const int pos = min(max(a.pos[(size_t)v * a.pos_stride], 0), a.max_ctx - 1);
+    if ((isq || isk) && a.rope_on) {
+        float partner[DL];
+        if constexpr (DL >= 2) {
+#pragma unroll
+            for (int j = 0; j < DL; j++) partner[j] = x[j ^ 1];
+        } else {
+            partner[0] = __shfl_xor(x[0], 1, 64);
+        }
+        float y[DL];
+#pragma unroll
+        for (int j = 0; j < DL; j++) {
+            const int i = lane * DL + j;
+            const float *cs = a.rope + ((size_t)pos * (dh / 2) + (i >> 1)) * 2;
+            const float c = act ? cs[0] : 1.0f, sn = act ? cs[1] : 0.0f;
+            y[j] = !(i & 1) ? x[j] * c - partner[j] * sn : partner[j] * sn + x[j] * c;
+        }
+#pragma unroll
+        for (int j = 0; j < DL; j++) x[j] = y[j];
+    }
+    if (!act) return;
+    if (isq) {
+#pragma unroll
+        for (int j = 0; j < DL; j++) a.q[(size_t)v * a.q_stride + row0 + lane * DL + j] = x[j];
+        return;
+    }
+    const int kvh = isk ? hh - a.n_heads : hh - a.n_heads - a.n_kv;
+    const size_t o = kv_offset(a.kv, v) + ((size_t)kvh * a.max_ctx + pos) * dh + lane * DL;
+    void *base = isk ? a.kv.k_base : a.kv.v_base;
+#pragma unroll
+    for (int j = 0; j < DL; j++) {
+        if (a.kv_f16) ((_Float16 *)base)[o + j] = (_Float16)x[j];
+        else ((float *)base)[o + j] = x[j];
+    }
+}
+
+int launch_qk_rope(const QkArgs &a, hipStream_t s)
+{
+    if (a.n < 1 || a.d_head < 16 || a.d_head > 256 || (a.d_head & (a.d_head - 1))) return -4;
+    const dim3 grid(a.n_heads + 2 * a.n_kv, a.n), block(64);
+    switch (a.d_head) {
+    case 256: hipLaunchKernelGGL(k_qk_rope<4>, grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL(k_qk_rope<2>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(k_qk_rope<1>, grid, block, 0, s, a); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int attn_max_splits(int max_ctx, int split) { return (max_ctx + split - 1) / split; }
 
 int launch_attn(const AttnArgs &a, hipStream_t s)

@@ -454,6 +454,7 @@ struct MLayer {
     int qkv_row0[3]{}, n_qkv = 1;
     cmolhip_qtensor_t o{}, gu{}, down{};
     float *attn_norm = nullptr, *ffn_norm = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;   // per-head QK-norm weights [d_head] or null
     int rope_on = 1;
 };
 
@@ -470,6 +471,7 @@ struct Batch {
     unsigned long long *argmax = nullptr;     // [cap][ARGMAX_SLOTS]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
     float *part = nullptr;                    // k-split partial sums of batched matvecs
+    float *qkv_raw = nullptr;                 // QK-norm models: [cap][d + 2 kvd] q|k|v rows
     int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
     unsigned long long *h_argmax = nullptr;   // pinned [cap][ARGMAX_SLOTS]
@@ -490,6 +492,7 @@ struct Prefill {
              *op_lm = nullptr;
     float *ss_a = nullptr, *ss_b = nullptr;   // [cap][d]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
+    float *qkv_raw = nullptr;                 // QK-norm models: [cap][d + 2 kvd]
     int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
     std::mutex mu;
@@ -610,6 +613,7 @@ int persist_format(const cmolhip_model_desc_t *d)
     if (dt != DT_Q4_0 && dt != DT_Q5_0 && dt != DT_Q8_0) return 0;   // no K-quant kernel
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &L = d->layers[l];
+        if (L.q_norm.data || L.k_norm.data) return 0;   // no QK-norm stage
         if (L.q.dtype != dt || L.k.dtype != dt || L.v.dtype != dt || L.o.dtype != dt ||
             L.gate.dtype != dt || L.down.dtype != dt)
             return 0;
@@ -671,9 +675,18 @@ int validate_desc(const cmolhip_model_desc_t *d)
         if (q8 != (L.k.dtype == DT_Q8_0) || q8 != (L.v.dtype == DT_Q8_0) || L.gate.dtype != L.up.dtype)
             return E_UNSUPPORTED;
         if (!chk_norm(L.attn_norm, h.d_model) || !chk_norm(L.ffn_norm, h.d_model)) return E_INVALID;
-        if (L.q_norm.data || L.k_norm.data) return E_UNSUPPORTED;
+        if ((L.q_norm.data && !chk_norm(L.q_norm, h.d_head)) || (L.k_norm.data && !chk_norm(L.k_norm, h.d_head)))
+            return E_INVALID;
     }
     return E_OK;
+}
+
+// Whether any layer normalises q or k per head (attn_q_norm / attn_k_norm).
+bool has_qk_norm(const cmolhip_model_desc_t *d)
+{
+    for (int l = 0; l < d->hp.n_layers; l++)
+        if (d->layers[l].q_norm.data || d->layers[l].k_norm.data) return true;
+    return false;
 }
 
 // Fold of the embedding / LM head (tied or not): the persistent kernel
@@ -746,11 +759,13 @@ void plan_batch(Plan &P, const cmolhip_model_desc_t *d, int cap, int ms)
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * h.d_head * 4);
     P.add(batch_part_floats(d, cap) * 4);
+    if (has_qk_norm(d)) P.add((size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head) * 4);
 }
 
 // Buffers of the prompt pass, in allocation order (mirrored by build_prefill).
-void plan_prefill(Plan &P, const cmolhip_hparams_t &h)
+void plan_prefill(Plan &P, const cmolhip_model_desc_t *d)
 {
+    const cmolhip_hparams_t &h = d->hp;
     const int cap = prefill_cap(h);
     const int ms = attn_max_splits(h.max_ctx, prefill_split(h.max_ctx));
     const size_t np = (size_t)h.n_kv_heads * ms * (h.n_heads / h.n_kv_heads);
@@ -768,6 +783,7 @@ void plan_prefill(Plan &P, const cmolhip_hparams_t &h)
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * h.d_head * 4);
+    if (has_qk_norm(d)) P.add((size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head) * 4);
 }
 
 
@@ -842,6 +858,8 @@ Plan make_plan(const cmolhip_model_desc_t *d)
         add_q(P, L.down.dtype, h.d_model, h.d_ffn, layer_fold(d, h.d_model, h.d_ffn));
         P.add((size_t)h.d_model * 4);
         P.add((size_t)h.d_model * 4);
+        if (L.q_norm.data) P.add((size_t)h.d_head * 4);
+        if (L.k_norm.data) P.add((size_t)h.d_head * 4);
     }
     add_q(P, d->embd.dtype, h.vocab, h.d_model, head_fold(d));
     if (d->lm_head.data) add_q(P, d->lm_head.dtype, h.vocab, h.d_model, head_fold(d));
@@ -854,7 +872,7 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add((size_t)h.n_kv_heads * h.max_ctx * h.d_head * 4);         // scratch
     for (int s = 0; s < h.max_sessions; s++) plan_batch(P, d, 1, ms);
     plan_batch(P, d, h.max_sessions, ms);                           // lock-step batch
-    plan_prefill(P, h);
+    plan_prefill(P, d);
     if (persist_format(d)) plan_persist(P, h);
     return P;
 }
@@ -875,6 +893,7 @@ struct cmolhip_model {
     std::unique_ptr<Prefill> pf;                 // prompt passes
     std::mutex scratch_mu;
     bool use_graph = true;
+    bool qk_norm = false;   // some layer normalises q or k per head
     // persistent single-session decode (pk_dt = layer format, 0: not used)
     int pk_dt = 0, pk_nwg = 0, pk_lds = 0;
     PkArgs pk{};                  // launch arguments but the per-step fields
@@ -923,6 +942,45 @@ ActIn act_in(const _Float16 *q, int n, const float *ss, int count, int stride, f
 
 const cmolhip_qtensor_t &lm_tensor(const cmolhip_model *m) { return m->lm.qs ? m->lm : m->embd; }
 
+// QKV of a QK-norm layer (src/attn.c:62-101): the matvec (or, for a prompt
+// pass, the GEMM) stores the raw q|k|v rows of each vector into `raw`, then
+// one stage normalises every q and k head, applies RoPE and writes q to
+// g.out and k / v to the cache.  g carries the activation operand, q output,
+// positions and the layer's RoPE switch.
+int enqueue_qk_norm(const cmolhip_model *m, const MLayer &L, GemvArgs g, float *raw, const KVRef &kv, int n,
+                    hipStream_t st, bool gemm)
+{
+    const cmolhip_hparams_t &hp = m->hp;
+    const int stride = hp.d_model + 2 * hp.n_kv_heads * hp.d_head;
+    QkArgs qa{};
+    qa.q = g.out;
+    qa.q_stride = g.out_stride;
+    g.out_stride = stride;
+    for (int r = 0; r < L.n_qkv; r++) {
+        g.w = to_qt(L.qkv[r]);
+        g.out = raw + L.qkv_row0[r];
+        g.row_base = 0;
+        RC(gemm ? launch_gemm(g, EPI_STORE, st) : launch_gemv(g, EPI_STORE, st));
+    }
+    qa.raw = raw;
+    qa.raw_stride = stride;
+    qa.qn_w = L.q_norm;
+    qa.kn_w = L.k_norm;
+    qa.eps = hp.rms_eps;
+    qa.n = n;
+    qa.n_heads = hp.n_heads;
+    qa.n_kv = hp.n_kv_heads;
+    qa.d_head = hp.d_head;
+    qa.max_ctx = hp.max_ctx;
+    qa.kv_f16 = hp.kv_f16;
+    qa.rope_on = L.rope_on;
+    qa.rope = m->rope;
+    qa.pos = g.pos;
+    qa.pos_stride = g.pos_stride;
+    qa.kv = kv;
+    return launch_qk_rope(qa, st);
+}
+
 // One decode step of n vectors of batch B (reference cmol_model_forward per
 // vector): embedding, L x (QKV+RoPE+KV write, attention, Wo + residual,
 // gate/up + SwiGLU, down + residual), LM head + argmax.
@@ -955,10 +1013,14 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         g.pos = B.steps + 1;
         g.pos_stride = 3;
         g.part = B.part;
-        for (int r = 0; r < L.n_qkv; r++) {   // one launch per run of q|k|v formats
-            g.w = to_qt(L.qkv[r]);
-            g.row_base = L.qkv_row0[r];
-            RC(launch_gemv(g, EPI_QKV, st));
+        if (L.q_norm || L.k_norm) {
+            RC(enqueue_qk_norm(m, L, g, B.qkv_raw, g.kv, n, st, false));
+        } else {
+            for (int r = 0; r < L.n_qkv; r++) {   // one launch per run of q|k|v formats
+                g.w = to_qt(L.qkv[r]);
+                g.row_base = L.qkv_row0[r];
+                RC(launch_gemv(g, EPI_QKV, st));
+            }
         }
 
         AttnArgs at{};
@@ -1065,10 +1127,14 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         g.kv = kv;
         g.pos = F.steps + 1;
         g.pos_stride = 3;
-        for (int r = 0; r < L.n_qkv; r++) {
-            g.w = to_qt(L.qkv[r]);
-            g.row_base = L.qkv_row0[r];
-            RC(launch_gemm(g, EPI_QKV, st));
+        if (L.q_norm || L.k_norm) {
+            RC(enqueue_qk_norm(m, L, g, F.qkv_raw, kv, n, st, true));
+        } else {
+            for (int r = 0; r < L.n_qkv; r++) {
+                g.w = to_qt(L.qkv[r]);
+                g.row_base = L.qkv_row0[r];
+                RC(launch_gemm(g, EPI_QKV, st));
+            }
         }
 
         AttnArgs at{};
@@ -1179,6 +1245,7 @@ int build_batch(cmolhip_model *m, Batch &B, int cap, size_t part_floats)
     RC(arena_get(c, (size_t)cap * np, &B.pl));
     RC(arena_get(c, (size_t)cap * np * h.d_head, &B.po));
     if (part_floats) RC(arena_get(c, part_floats, &B.part));
+    if (m->qk_norm) RC(arena_get(c, (size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head), &B.qkv_raw));
     HC(hipMemsetAsync(B.steps, 0, (size_t)cap * 12, c->stream));
     HC(hipStreamCreateWithFlags(&B.st, hipStreamNonBlocking));
     HC(hipHostMalloc((void **)&B.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
@@ -1208,6 +1275,7 @@ int build_prefill(cmolhip_model *m, Prefill &F)
     RC(arena_get(c, (size_t)cap * np, &F.pm));
     RC(arena_get(c, (size_t)cap * np, &F.pl));
     RC(arena_get(c, (size_t)cap * np * h.d_head, &F.po));
+    if (m->qk_norm) RC(arena_get(c, (size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head), &F.qkv_raw));
     HC(hipHostMalloc((void **)&F.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
     HC(hipHostMalloc((void **)&F.h_slots, (size_t)cap * 4, hipHostMallocDefault));
     return E_OK;
@@ -1359,6 +1427,7 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
     const cmolhip_hparams_t &h = d->hp;
     void *stg = nullptr;
     RC(cmolhip_alloc(c, P.staging, ALIGN, &stg));
+    m->qk_norm = has_qk_norm(d);
     m->layers.resize(h.n_layers);
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &T = d->layers[l];
@@ -1385,6 +1454,8 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
                     P.staging, &L.down));
         RC(upload_norm(c, T.attn_norm, &L.attn_norm));
         RC(upload_norm(c, T.ffn_norm, &L.ffn_norm));
+        if (T.q_norm.data) RC(upload_norm(c, T.q_norm, &L.q_norm));
+        if (T.k_norm.data) RC(upload_norm(c, T.k_norm, &L.k_norm));
         L.rope_on = !(h.no_rope_interval > 0 && (l + 1) % h.no_rope_interval == 0);
     }
     const cmolhip_host_tensor_t *e[1] = {&d->embd};

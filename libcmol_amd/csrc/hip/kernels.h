@@ -273,6 +273,24 @@ struct AttnArgs {
 };
 
 int launch_attn(const AttnArgs &a, hipStream_t s);
+
+// QK-norm models (src/attn.c:62-101): the QKV matvec stores raw q|k|v rows;
+// this stage normalises each q and k head (RMSNorm over d_head, weights
+// shared by the heads), applies RoPE and writes q and the KV cache.
+struct QkArgs {
+    const float *raw;        // [n][raw_stride]: q rows, then k, then v
+    int raw_stride;
+    float *q;                // [n][q_stride]
+    int q_stride;
+    const float *qn_w, *kn_w;   // [d_head] or nullptr (no norm of that part)
+    float eps;
+    int n, n_heads, n_kv, d_head, max_ctx, kv_f16, rope_on;
+    const float *rope;       // [max_ctx][d_head/2][2]
+    const int32_t *pos;      // pos[v * pos_stride]
+    int pos_stride;
+    KVRef kv;
+};
+int launch_qk_rope(const QkArgs &a, hipStream_t s);
 int attn_max_splits(int max_ctx, int split);
 
 // ---- persist_q4/q5/q8.hip: the persistent single-session decode kernel

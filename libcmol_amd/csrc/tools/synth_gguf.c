@@ -37,6 +37,7 @@ typedef struct {
     int32_t wtype, embd_type, out_type;   /* out_type < 0: tied embeddings */
     int32_t nope_interval, eos_id, qk_norm, arch_smollm3, transcode_q8;
     int32_t v_type, down_type;            /* attn_v / ffn_down format (< 0: wtype) */
+    int32_t rope_scaling;                 /* 1: write <arch>.rope.scaling.type = "yarn" */
     float rope_base, rms_eps, wstd, norm_jitter;
     uint64_t seed;
 } cmolsynth_spec_t;
@@ -456,7 +457,7 @@ static int write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads,
     FILE *f = fopen(path, "wb");
     if (!f) { free(td); return -2; }
     const char *arch = s->arch_smollm3 ? "smollm3" : "llama";
-    int n_kv = 12 + (s->nope_interval > 0);
+    int n_kv = 12 + (s->nope_interval > 0) + (s->rope_scaling > 0);
     if (tk)
         n_kv += (tk->types != NULL) + (tk->n_merges > 0) + (tk->bos_id >= 0) + (tk->eos_id >= 0) +
                 (tk->unk_id >= 0) + (tk->add_bos >= 0);
@@ -479,6 +480,7 @@ static int write_gguf(const char *path, const cmolsynth_spec_t *s, int nthreads,
     kv_f32(f, AKEY("attention.layer_norm_rms_epsilon"), s->rms_eps);
     kv_u32(f, AKEY("vocab_size"), (uint32_t)s->vocab);
     if (s->nope_interval > 0) kv_u32(f, AKEY("attention.no_rope_layer_interval"), (uint32_t)s->nope_interval);
+    if (s->rope_scaling > 0) kv_str(f, AKEY("rope.scaling.type"), "yarn");
 #undef AKEY
     if (!tk) {
         kv_str(f, "tokenizer.ggml.model", "llama");

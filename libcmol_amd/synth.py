@@ -23,7 +23,7 @@ class _Spec(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_layers", "d_model", "n_heads", "n_kv_heads", "d_ffn", "vocab", "ctx_len",
         "wtype", "embd_type", "out_type", "nope_interval", "eos_id", "qk_norm",
-        "arch_smollm3", "transcode_q8", "v_type", "down_type")] + [
+        "arch_smollm3", "transcode_q8", "v_type", "down_type", "rope_scaling")] + [
         ("rope_base", C.c_float), ("rms_eps", C.c_float), ("wstd", C.c_float),
         ("norm_jitter", C.c_float), ("seed", C.c_uint64)]
 
@@ -68,6 +68,7 @@ class ModelSpec:
     transcode_q8: int = 0         # write Q4_0/Q5_0 tensors as lossless Q8_0
     v_type: int = -1              # attn_v format (-1: wtype)
     down_type: int = -1           # ffn_down format (-1: wtype)
+    rope_scaling: int = 0         # 1: a rope.scaling.type = "yarn" key (recorded, not applied)
     rope_base: float = 10000.0
     rms_eps: float = 1e-5
     wstd: float = 0.02

@@ -11,6 +11,7 @@ import pytest
 
 from libcmol_amd import synth
 from oracle import oracle as O
+from tests.golden import make_qknorm_golden as qkn
 from tests.qdata import random_blocks
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -137,6 +138,38 @@ def test_kquant_models_match_reference(preset, model_dir):
     assert np.array_equal(prompt, synth.tokens(16, 42, spec.vocab))
     got = O.Model(path, 128).generate(prompt, 48)
     assert got.tolist() == KQ[f"model_{preset}_ids"].tolist()
+
+
+# ---- QK-norm (tests/golden/make_qknorm_golden.py) ---------------------------
+QN = np.load(os.path.join(HERE, "golden", "qknorm.npz"))
+
+
+@pytest.mark.parametrize("name", sorted(qkn.MODELS))
+def test_qk_norm_models_match_reference(name, model_dir):
+    """Models with attn_q_norm / attn_k_norm (per-head RMSNorm of q and k
+    before RoPE; d_head 64 and 128, with NoPE layers, Q8_0 / Q5_0 / Q4_K):
+    the oracle's logits after the prompt and its greedy continuation equal
+    the reference's."""
+    spec = qkn.spec_of(name)
+    path = synth.model_file(spec, model_dir)
+    prompt = QN[f"{name}_prompt"]
+    om = O.Model(path, 128)
+    for p, t in enumerate(prompt):
+        lg = om.forward(int(t), p)
+    want = QN[f"{name}_prompt_logits"]
+    assert np.all(np.abs(lg - want) <= 1e-5 + 1e-4 * np.abs(want))
+    got = O.Model(path, 128).generate(prompt, 40)
+    assert got.tolist() == QN[f"{name}_ids"].tolist()
+
+
+def test_yarn_key_is_not_applied(model_dir):
+    """A rope.scaling.type key is recorded and ignored by the reference
+    (src/gguf.c:384-389): the SmolLM3-shaped fixture model decodes exactly as
+    the same weights without the key."""
+    spec = qkn.spec_of("qkn_smollm3_yarn")
+    prompt = QN["qkn_smollm3_yarn_prompt"]
+    plain = synth.model_file(spec.replace(rope_scaling=0), model_dir)
+    assert O.Model(plain, 128).generate(prompt, 40).tolist() == QN["qkn_smollm3_yarn_ids"].tolist()
 
 
 def test_q4_k_closed_form():
