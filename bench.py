@@ -179,6 +179,52 @@ def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
             "kv_bytes_per_step": kv_bytes}
 
 
+def bench_generate_concurrent(path, spec, sessions, new_tokens, lo=512, hi=16384):
+    """The public path with one thread per session: `sessions` concurrent
+    cmol_generate callers (greedy, token ids) over the same log-uniform
+    synthetic contexts as decode_32; the library's scheduler batches their
+    decode steps.  Wall clock from the first call to the last return,
+    including each caller's one-token prompt pass."""
+    import threading
+    lens = synth.log_uniform_lengths(sessions, lo, hi, seed=7)
+    max_ctx = int(lens.max()) + new_tokens + 8
+    os.environ["CMOL_KV_F16"] = "1"
+    try:
+        m = native.Model(path, max_ctx=max_ctx, max_sessions=sessions)
+    finally:
+        os.environ.pop("CMOL_KV_F16", None)
+    ss = [m.acquire() for _ in range(sessions)]
+    prm = native.greedy_params(new_tokens)
+    prompts = [synth.tokens(1, 40 + i, spec.vocab) for i in range(sessions)]
+    got = [0] * sessions
+
+    def run(i):
+        got[i] = len(ss[i].generate_ids(prompts[i], prm, new_tokens))
+
+    def once():
+        for i, s in enumerate(ss):
+            s.reset()
+            s.fill_kv(int(lens[i]), seed=100 + i)
+        hiprt.device_synchronize()
+        th = [threading.Thread(target=run, args=(i,)) for i in range(sessions)]
+        t0 = time.perf_counter()
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        return time.perf_counter() - t0
+
+    once()   # warm-up: first batches of each size
+    _, b0, s0, _ = m.sched_stats()
+    wall = once()
+    _, b1, s1, largest = m.sched_stats()
+    m.close()
+    tokens = sum(got)
+    return {"tok_s": tokens / wall, "wall_s": wall, "sessions": sessions, "new_tokens": new_tokens,
+            "tokens": tokens, "batches": b1 - b0, "mean_batch": (s1 - s0) / max(b1 - b0, 1),
+            "largest_batch": largest, "mean_ctx": float(np.mean(lens))}
+
+
 def recorded_traffic(name):
     """HBM bytes per launch of the roofline kernel from its counter summary
     under profiles/ (two rocprofv3 counter passes, FETCH_SIZE and WRITE_SIZE,
@@ -234,7 +280,8 @@ def main():
     ap.add_argument("--sessions", type=int, default=32)
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
-    ap.add_argument("--skip", default="", help="comma list of: decode,multi,matvec,gemm,cpu")
+    ap.add_argument("--generate-tokens", type=int, default=48)
+    ap.add_argument("--skip", default="", help="comma list of: decode,multi,generate,matvec,gemm,cpu")
     ap.add_argument("--synthetic-context", type=int, default=0,
                     help="decode after filling the KV cache with this many synthetic positions "
                          "instead of a prefill (profiling runs)")
@@ -286,6 +333,11 @@ def main():
         log("32-session decode")
         d32 = bench_decode_32(path, spec, args.sessions, args.multi_steps, 2)
         log(json.dumps(d32))
+    g32 = None
+    if "generate" not in skip:
+        log("32 concurrent cmol_generate callers")
+        g32 = bench_generate_concurrent(path, spec, args.sessions, args.generate_tokens)
+        log(json.dumps(g32))
     cpu = None
     if "cpu" not in skip:
         log("cpu baseline")
@@ -327,6 +379,7 @@ def main():
                    "effective_weight_GBps": round(weight_bytes * d1["tok_s"] / 1e9, 1)},
         "decode_1": d1,
         "decode_32": d32,
+        "generate_32": g32,
         "matvec": mv,
         "prefill_gemm": gm,
         "roofline": roof,

@@ -11,6 +11,10 @@
  *                          sessions (the reference runs one thread per session)
  *   cmol__session_fill_kv  no reference counterpart: synthetic KV contents of a
  *                          given length, for long-context benchmarks
+ *   cmol__sched_stats,     no reference counterpart: counters and a device-free
+ *   cmol__sched_selftest   self-test of the scheduler that batches concurrent
+ *                          cmol_generate decode steps (the reference runs each
+ *                          caller's steps alone, src/api.c:443-521)
  */
 #ifndef CMOL_EXT_H
 #define CMOL_EXT_H
@@ -63,6 +67,21 @@ void cmol_apply_repeat_penalty(float *logits, int vocab_size, const int32_t *tok
  * parity checks on machines without a GPU).  Same errors as cmol_load's
  * parse stage. */
 cmol_model_t *cmol__load_text(const char *path, cmol_err_t *err);
+
+/* Counters of the cross-session scheduler: out[0] batches run, out[1] steps
+ * in them, out[2] the largest batch.  Returns 1 when the model batches
+ * concurrent decode steps (max_sessions > 1 and CMOL_BATCH is not 0), 0 when
+ * it does not (counters 0), or a negative cmol_err_t. */
+int cmol__sched_stats(cmol_model_t *m, uint64_t out[3]);
+
+/* The scheduler's rendezvous without a device: `threads` posters (thread i
+ * leaves after steps + i steps, with 0..host_us µs of host work between its
+ * steps) against a stand-in batch that takes device_us µs; wait_us is the
+ * straggler window.  stats as in cmol__sched_stats.  Returns the count of
+ * wrong results (0 when every poster got its own answer and no batch held a
+ * session twice) or a negative cmol_err_t. */
+int cmol__sched_selftest(int threads, int steps, long wait_us, long device_us, unsigned host_us,
+                         uint64_t stats[3]);
 
 int cmol__session_length(const cmol_session_t *s);
 int cmol__session_slot(const cmol_session_t *s);

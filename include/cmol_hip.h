@@ -187,10 +187,17 @@ int cmolhip_persist_trace(cmolhip_model_t *m, uint64_t *out, int cap);
  * own stores drained.  Returns the work-group count, CMOL_ERR_TRUNC when
  * cap is too small. */
 int cmolhip_persist_marks(cmolhip_model_t *m, uint64_t *out, size_t cap);
-/* Lock-step decode of n sessions (distinct slots, each at its own pos). */
+/* Lock-step decode of n sessions (distinct slots, each at its own pos).
+ * logits_host: NULL or [n][vocab]. */
 int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots,
                          const int32_t *tokens, const int32_t *pos,
                          float *logits_host, int32_t *argmax);
+/* As cmolhip_decode_batch, with each vector's logits copied to its own host
+ * buffer: logits_each NULL, or n pointers each NULL (no copy) or [vocab]
+ * (the cross-session scheduler hands each session its own logits). */
+int cmolhip_decode_batch_each(cmolhip_model_t *m, int n, const int32_t *slots,
+                              const int32_t *tokens, const int32_t *pos,
+                              float *const *logits_each, int32_t *argmax);
 /* Prompt of n tokens at positions pos0.. into session `slot`, in batched
  * passes of prefill_chunk tokens (prompt GEMMs on MFMA, causal attention
  * over the cache); outputs as in cmolhip_decode for the last prompt token. */

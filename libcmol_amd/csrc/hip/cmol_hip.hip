@@ -500,6 +500,18 @@ struct Prefill {
 
 constexpr int ATTN_SPLIT_MIN = 64, ATTN_SPLIT_MAX = 1024;
 
+// Prompts of up to this many tokens run through the matvec kernels as one
+// lock-step batch of the session's consecutive positions: at this size the
+// tiled GEMM covers too few work-groups (a 1-token pass costs 5x a decode
+// step at the 3B shape).
+constexpr int PROMPT_MATVEC_MAX = 8;
+
+// Vectors of the shared lock-step batch: every session, and short prompts.
+int multi_cap(const cmolhip_hparams_t &h)
+{
+    return h.max_sessions > PROMPT_MATVEC_MAX ? h.max_sessions : PROMPT_MATVEC_MAX;
+}
+
 int prefill_cap(const cmolhip_hparams_t &h)
 {
     const int c = h.prefill_chunk > 0 ? h.prefill_chunk : 512;
@@ -871,7 +883,7 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(kv_elems * esz);
     P.add((size_t)h.n_kv_heads * h.max_ctx * h.d_head * 4);         // scratch
     for (int s = 0; s < h.max_sessions; s++) plan_batch(P, d, 1, ms);
-    plan_batch(P, d, h.max_sessions, ms);                           // lock-step batch
+    plan_batch(P, d, multi_cap(h), ms);                             // lock-step batch
     plan_prefill(P, d);
     if (persist_format(d)) plan_persist(P, h);
     return P;
@@ -1487,7 +1499,7 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
         RC(cmolhip_memcpy_h2d(c, B.slot_ids, &sid, 4));
     }
     m->multi.reset(new Batch());
-    RC(build_batch(m, *m->multi, h.max_sessions, batch_part_floats(d, h.max_sessions)));
+    RC(build_batch(m, *m->multi, multi_cap(h), batch_part_floats(d, multi_cap(h))));
     m->pf.reset(new Prefill());
     RC(build_prefill(m, *m->pf));
     if (persist_format(d)) RC(build_persist(m, persist_format(d)));
@@ -1522,11 +1534,16 @@ int run_single(cmolhip_model *m, Batch &B)
     return enqueue_step(m, B, 1, B.st);
 }
 
-int finish(cmolhip_model *m, Batch &B, int n, float *logits_host, int32_t *argmax)
+int finish(cmolhip_model *m, Batch &B, int n, float *logits_host, int32_t *argmax,
+           float *const *logits_each = nullptr)
 {
     HC(hipMemcpyAsync(B.h_argmax, B.argmax, (size_t)n * ARGMAX_SLOTS * 8, hipMemcpyDeviceToHost, B.st));
-    if (logits_host)
-        HC(hipMemcpyAsync(logits_host, B.logits, (size_t)n * m->hp.vocab * 4, hipMemcpyDeviceToHost, B.st));
+    const size_t V = m->hp.vocab;
+    if (logits_host) HC(hipMemcpyAsync(logits_host, B.logits, n * V * 4, hipMemcpyDeviceToHost, B.st));
+    if (logits_each)
+        for (int i = 0; i < n; i++)
+            if (logits_each[i])
+                HC(hipMemcpyAsync(logits_each[i], B.logits + i * V, V * 4, hipMemcpyDeviceToHost, B.st));
     HC(hipStreamSynchronize(B.st));
     if (argmax)
         for (int i = 0; i < n; i++)
@@ -1543,6 +1560,40 @@ void destroy_batch(Batch &B)
     if (B.h_steps) (void)hipHostFree(B.h_steps);
     if (B.h_slots) (void)hipHostFree(B.h_slots);
     if (B.h_argmax) (void)hipHostFree(B.h_argmax);
+}
+
+int decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t *tokens, const int32_t *pos,
+                 float *logits_host, float *const *logits_each, int32_t *argmax);
+
+// A short prompt of session `slot` as one lock-step step of the matvec path:
+// vector i is tokens[i] at pos0 + i in the same cache.  The QKV kernel writes
+// every vector's K/V before the attention kernel reads positions < pos + 1,
+// so vector i attends to the prompt's earlier tokens as in a causal pass.
+// Outputs (logits, argmax) are the last vector's.
+int prompt_by_matvec(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, int32_t pos0,
+                     float *logits_host, int32_t *argmax)
+{
+    Batch &B = *m->multi;
+    if (n > B.cap) return E_ARGS;
+    std::lock_guard<std::mutex> g(B.mu);   // same order as decode_batch: batch, then slot
+    std::lock_guard<std::mutex> gs(m->slots[slot]->mu);
+    for (int i = 0; i < n; i++) {
+        B.h_steps[3 * i + 0] = tokens[i];
+        B.h_steps[3 * i + 1] = pos0 + i;
+        B.h_steps[3 * i + 2] = pos0 + i + 1;
+        B.h_slots[i] = slot;
+    }
+    HC(hipMemcpyAsync(B.steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
+    HC(hipMemcpyAsync(B.slot_ids, B.h_slots, (size_t)n * 4, hipMemcpyHostToDevice, B.st));
+    RC(enqueue_step(m, B, n, B.st));
+    const size_t V = m->hp.vocab;
+    HC(hipMemcpyAsync(B.h_argmax, B.argmax + (size_t)(n - 1) * ARGMAX_SLOTS, ARGMAX_SLOTS * 8,
+                      hipMemcpyDeviceToHost, B.st));
+    if (logits_host)
+        HC(hipMemcpyAsync(logits_host, B.logits + (n - 1) * V, V * 4, hipMemcpyDeviceToHost, B.st));
+    HC(hipStreamSynchronize(B.st));
+    if (argmax) *argmax = (int32_t)argmax_index(reduce_slots(B.h_argmax));
+    return E_OK;
 }
 
 } // namespace
@@ -1650,6 +1701,8 @@ int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, 
     if (pos0 < 0 || (long)pos0 + n > m->hp.max_ctx) return E_ARGS;
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->hp.vocab) return E_ARGS;
+    if (n == 1) return cmolhip_decode(m, slot, tokens[0], pos0, logits_host, argmax);
+    if (n <= PROMPT_MATVEC_MAX) return prompt_by_matvec(m, slot, tokens, n, pos0, logits_host, argmax);
     Batch &B = *m->slots[slot];
     Prefill &F = *m->pf;
     std::lock_guard<std::mutex> g(B.mu);
@@ -1673,6 +1726,22 @@ int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, 
 
 int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t *tokens,
                          const int32_t *pos, float *logits_host, int32_t *argmax)
+{
+    return decode_batch(m, n, slots, tokens, pos, logits_host, nullptr, argmax);
+}
+
+int cmolhip_decode_batch_each(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t *tokens,
+                              const int32_t *pos, float *const *logits_each, int32_t *argmax)
+{
+    return decode_batch(m, n, slots, tokens, pos, nullptr, logits_each, argmax);
+}
+
+} // extern "C"
+
+namespace {
+
+int decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t *tokens, const int32_t *pos,
+                 float *logits_host, float *const *logits_each, int32_t *argmax)
 {
     if (!m || n < 1 || n > m->hp.max_sessions || !slots || !tokens || !pos) return E_ARGS;
     for (int i = 0; i < n; i++) {
@@ -1698,8 +1767,12 @@ int cmolhip_decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const 
     HC(hipMemcpyAsync(B.steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
     HC(hipMemcpyAsync(B.slot_ids, B.h_slots, (size_t)n * 4, hipMemcpyHostToDevice, B.st));
     RC(enqueue_step(m, B, n, B.st));
-    return finish(m, B, n, logits_host, argmax);
+    return finish(m, B, n, logits_host, argmax, logits_each);
 }
+
+} // namespace
+
+extern "C" {
 
 int cmolhip_kv_download(cmolhip_model_t *m, int slot, int layer, int n, float *k_out, float *v_out)
 {

@@ -82,6 +82,53 @@ static int env_kv_f16(void)
     return e && e[0] == '1';
 }
 
+/* Cross-session batching of concurrent decode steps (sched.c): on unless
+ * CMOL_BATCH=0; CMOL_BATCH_WAIT_US sets how long a posted step waits for the
+ * other active sessions (default 2000 µs, about one decode step of a 3B
+ * model). */
+static int env_batch(void)
+{
+    const char *e = getenv("CMOL_BATCH");
+    return !(e && e[0] == '0');
+}
+
+static long env_batch_wait_us(void)
+{
+    const char *e = getenv("CMOL_BATCH_WAIT_US");
+    long v = e ? atol(e) : 2000;
+    return v < 0 ? 0 : v > 1000000 ? 1000000 : v;
+}
+
+/* The scheduler's batch: one session through its own decode graph, more as
+ * one lock-step batch (each session's logits to its own buffer). */
+static int run_steps(void *ctx, cmol_step_t *const *st, int n)
+{
+    cmol_model_t *m = (cmol_model_t *)ctx;
+    int rc;
+    if (n == 1) {
+        int32_t next = 0;
+        rc = cmolhip_decode(m->dev, st[0]->slot, st[0]->token, st[0]->pos, st[0]->logits, &next);
+        st[0]->next = next;
+        st[0]->rc = rc;
+        return rc;
+    }
+    int32_t slots[CMOL_MAX_SESSIONS] = {0}, tokens[CMOL_MAX_SESSIONS] = {0}, pos[CMOL_MAX_SESSIONS] = {0},
+            next[CMOL_MAX_SESSIONS] = {0};
+    float *lg[CMOL_MAX_SESSIONS] = {0};
+    for (int i = 0; i < n; i++) {
+        slots[i] = st[i]->slot;
+        tokens[i] = st[i]->token;
+        pos[i] = st[i]->pos;
+        lg[i] = st[i]->logits;
+    }
+    rc = cmolhip_decode_batch_each(m->dev, n, slots, tokens, pos, lg, next);
+    for (int i = 0; i < n; i++) {
+        st[i]->next = rc ? 0 : next[i];
+        st[i]->rc = rc;
+    }
+    return rc;
+}
+
 static cmolhip_host_tensor_t host_tensor(const cmol_tensor_t *t)
 {
     cmolhip_host_tensor_t h;
@@ -267,6 +314,13 @@ static cmol_model_t *load_model(const char *path, const cmol_config_t *cfg, cmol
     }
     m->pool_free = c.max_sessions == 32 ? 0xFFFFFFFFu : (1u << c.max_sessions) - 1u;
     if (pthread_mutex_init(&m->pool_lock, NULL) != 0) FAIL(CMOL_ERR_OOM);
+    if (c.max_sessions > 1 && env_batch()) {
+        if (cmol_sched_init(&m->sched, run_steps, m, env_batch_wait_us()) != CMOL_OK) {
+            pthread_mutex_destroy(&m->pool_lock);
+            FAIL(CMOL_ERR_OOM);
+        }
+        m->sched_on = 1;
+    }
 #undef FAIL
     cmol_log(m, CMOL_LOG_INFO,
              "cmol_load: arch=%s layers=%d heads=%d/%d d=%d ffn=%d vocab=%d ctx=%d sessions=%d "
@@ -292,6 +346,7 @@ void cmol_free(cmol_model_t *m)
 {
     if (!m) return;
     pthread_mutex_destroy(&m->pool_lock);
+    if (m->sched_on) cmol_sched_destroy(&m->sched);
     cmolhip_model_destroy(m->dev);
     cmol_mmap_close(&m->mmap);
     free(m->arena_buf);
@@ -393,8 +448,21 @@ static cmol_err_t generate_core(cmol_session_t *s, int n_prompt, const cmol_gen_
     if (n_prompt > avail) n_prompt = avail;
     int pos = s->n_tokens;
     int32_t dev_next = 0;
-    int drc = cmolhip_prefill(m->dev, s->slot, s->token_buf, n_prompt, pos,
-                              host_logits ? s->logits : NULL, &dev_next);
+    int drc;
+    /* A caller joins the scheduler's batches once its prompt is in (a long
+     * prompt pass would hold the others' steps); a one-token prompt is a
+     * decode step and joins at once. */
+    const int batch_prompt = m->sched_on && n_prompt == 1;
+    if (batch_prompt) {
+        cmol_sched_enter(&m->sched);
+        cmol_step_t st = {s->slot, s->token_buf[0], pos, host_logits ? s->logits : NULL, 0, 0, 0};
+        drc = cmol_sched_step(&m->sched, &st);
+        dev_next = st.next;
+        if (drc != 0) cmol_sched_leave(&m->sched);
+    } else {
+        drc = cmolhip_prefill(m->dev, s->slot, s->token_buf, n_prompt, pos, host_logits ? s->logits : NULL,
+                              &dev_next);
+    }
     if (drc != 0) return (cmol_err_t)drc;
     pos += n_prompt;
     s->n_tokens = pos;
@@ -414,6 +482,8 @@ static cmol_err_t generate_core(cmol_session_t *s, int n_prompt, const cmol_gen_
         fill = seed_n;
     }
     int produced = 0;
+    cmol_err_t out = CMOL_OK;
+    if (m->sched_on && !batch_prompt) cmol_sched_enter(&m->sched);
     for (;;) {
         int32_t next;
         if (host_logits) {
@@ -432,12 +502,22 @@ static cmol_err_t generate_core(cmol_session_t *s, int n_prompt, const cmol_gen_
         produced++;
         if (max_new > 0 && produced >= max_new) break;
         if (pos >= s->max_tokens) break;
-        drc = cmolhip_decode(m->dev, s->slot, next, pos, host_logits ? s->logits : NULL, &dev_next);
-        if (drc != 0) return (cmol_err_t)drc;
+        if (m->sched_on) {   /* batched with the other sessions' steps */
+            cmol_step_t st = {s->slot, next, pos, host_logits ? s->logits : NULL, 0, 0, 0};
+            drc = cmol_sched_step(&m->sched, &st);
+            dev_next = st.next;
+        } else {
+            drc = cmolhip_decode(m->dev, s->slot, next, pos, host_logits ? s->logits : NULL, &dev_next);
+        }
+        if (drc != 0) {
+            out = (cmol_err_t)drc;
+            break;
+        }
         pos++;
         s->n_tokens = pos;
     }
-    return CMOL_OK;
+    if (m->sched_on) cmol_sched_leave(&m->sched);
+    return out;
 }
 
 typedef struct {
@@ -547,6 +627,17 @@ int cmol__session_fill_kv(cmol_session_t *s, int n_tokens, uint64_t seed)
     if (rc) return rc;
     s->n_tokens = n_tokens;
     return CMOL_OK;
+}
+
+int cmol__sched_stats(cmol_model_t *m, uint64_t out[3])
+{
+    if (!m || !out) return CMOL_ERR_ARGS;
+    if (!m->sched_on) {
+        out[0] = out[1] = out[2] = 0;
+        return 0;
+    }
+    cmol_sched_stats(&m->sched, out);
+    return 1;
 }
 
 int cmol__session_length(const cmol_session_t *s) { return s ? s->n_tokens : CMOL_ERR_ARGS; }

@@ -85,6 +85,33 @@ typedef struct {
     size_t size;
 } cmol_mmap_t;
 
+/* One decode step posted to the cross-session scheduler (sched.c). */
+typedef struct cmol_step {
+    int slot;                 /* device session slot */
+    int32_t token, pos;
+    float *logits;            /* host logits wanted here, or NULL */
+    int32_t next;             /* out: argmax of the logits */
+    int rc;                   /* out: 0 or a cmol_err_t */
+    int done;
+} cmol_step_t;
+
+/* Runs n posted steps (distinct slots) as one batch; sets next / rc. */
+typedef int (*cmol_batch_fn)(void *ctx, cmol_step_t *const *steps, int n);
+
+typedef struct {
+    pthread_mutex_t mu;
+    pthread_cond_t cv;        /* CLOCK_MONOTONIC */
+    int ready;
+    int active;               /* callers inside their decode loop */
+    int running;              /* a batch is in flight */
+    int n_pending;
+    cmol_step_t *pending[CMOL_MAX_SESSIONS];
+    uint64_t wait_ns, idle_since_ns;
+    uint64_t batches, steps, max_batch;
+    cmol_batch_fn run;
+    void *ctx;
+} cmol_sched_t;
+
 struct cmol_model {
     cmol_hparams_t hparams;
     cmol_mmap_t mmap;
@@ -99,6 +126,8 @@ struct cmol_model {
     uint32_t pool_free;
     cmolhip_model_t *dev;     /* device weights, KV caches, decode graphs */
     int kv_f16;
+    cmol_sched_t sched;       /* batches concurrent decode steps (max_sessions > 1) */
+    int sched_on;
 };
 
 struct cmol_session {
@@ -133,6 +162,14 @@ int cmol_tokenizer_encode(const cmol_tokenizer_t *tok, const char *text, int32_t
                           int out_cap, int add_bos);
 const char *cmol_tokenizer_decode_token(const cmol_tokenizer_t *tok, int32_t id);
 size_t cmol_tokenizer_arena_bytes(int vocab_size, int n_merges_hint);
+
+/* sched.c */
+int cmol_sched_init(cmol_sched_t *q, cmol_batch_fn run, void *ctx, long wait_us);
+void cmol_sched_destroy(cmol_sched_t *q);
+void cmol_sched_enter(cmol_sched_t *q);
+void cmol_sched_leave(cmol_sched_t *q);
+int cmol_sched_step(cmol_sched_t *q, cmol_step_t *st);
+void cmol_sched_stats(cmol_sched_t *q, uint64_t out[3]);
 
 /* sampler.c */
 int32_t cmol_sample(float *logits, int vocab_size, const cmol_gen_params_t *params,

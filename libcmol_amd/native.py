@@ -99,6 +99,7 @@ SIGNATURES = [
     ("cmolhip_model_ctx", P, [P]),
     ("cmolhip_decode", C.c_int, [P, C.c_int, I32, I32, P, P]),
     ("cmolhip_decode_batch", C.c_int, [P, C.c_int, P, P, P, P, P]),
+    ("cmolhip_decode_batch_each", C.c_int, [P, C.c_int, P, P, P, P, P]),
     ("cmolhip_prefill", C.c_int, [P, C.c_int, P, C.c_int, I32, P, P]),
     ("cmolhip_kv_download", C.c_int, [P, C.c_int, C.c_int, C.c_int, P, P]),
     ("cmolhip_kv_upload", C.c_int, [P, C.c_int, C.c_int, C.c_int, P, P]),
@@ -118,6 +119,8 @@ SIGNATURES = [
     ("cmol_rng_seed", None, [P, C.c_uint]),
     ("cmol_rng_next", C.c_uint64, [P]),
     ("cmol_apply_repeat_penalty", None, [P, C.c_int, P, C.c_int, C.c_float]),
+    ("cmol__sched_stats", C.c_int, [P, P]),
+    ("cmol__sched_selftest", C.c_int, [C.c_int, C.c_int, C.c_long, C.c_long, C.c_uint, P]),
     ("cmol__session_length", C.c_int, [P]),
     ("cmol__session_slot", C.c_int, [P]),
     ("cmol__device", P, [P]),
@@ -277,6 +280,13 @@ class Model:
             self.close()
         except Exception:
             pass
+
+    def sched_stats(self):
+        """(batching on, batches, steps, largest batch) of the scheduler that
+        batches concurrent decode steps."""
+        out = np.zeros(3, np.uint64)
+        on = check(lib().cmol__sched_stats(self.h, ptr(out)), "sched_stats")
+        return bool(on), int(out[0]), int(out[1]), int(out[2])
 
     def acquire(self) -> "Session":
         s = lib().cmol_session_acquire(self.h)

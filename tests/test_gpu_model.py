@@ -241,3 +241,35 @@ def test_mixed_qkv_formats(gpu, model_dir):
     bad = synth.model_file(synth.PRESETS["small-q4_0"].replace(v_type=synth.Q8_0), model_dir)
     with pytest.raises(RuntimeError, match=str(native.CMOL_ERR_UNSUPPORTED)):
         native.Model(bad, max_ctx=64, max_sessions=1)
+
+
+@pytest.mark.parametrize("preset,sessions", [("small-q4_0", 1), ("small-q4_k_m", 3), ("micro-q8_0", 1)])
+def test_short_prompts_match_oracle(gpu, model_dir, preset, sessions):
+    """Prompts of 1..8 tokens run through the matvec kernels (one lock-step
+    step over the session's consecutive positions), after a longer first
+    turn: logits after each prompt and the session's KV cache match the
+    oracle's token-by-token forward."""
+    spec = synth.PRESETS[preset].replace(wstd=0.08)
+    path = synth.model_file(spec, model_dir)
+    m = native.Model(path, max_ctx=96, max_sessions=sessions)
+    s = m.acquire()
+    om = O.Model(path, 96)
+    pos = 0
+    for turn, n in enumerate([12, 1, 2, 5, 8, 3]):
+        toks = synth.tokens(n, 500 + turn, spec.vocab)
+        am, lg = s.prefill(toks, spec.vocab)
+        for t in toks:
+            want = om.forward(int(t), pos)
+            pos += 1
+        assert close_frac(lg, want) == 1.0, f"turn {turn} ({n} tokens)"
+        assert am == int(np.argmax(lg))
+    ok, ov = om.kv()
+    kd = spec.n_kv_heads * spec.d_head
+    for layer in range(spec.n_layers):
+        k = np.zeros((pos, kd), np.float32)
+        v = np.zeros((pos, kd), np.float32)
+        native.check(native.lib().cmolhip_kv_download(m.device, s.slot, layer, pos,
+                                                       native.ptr(k), native.ptr(v)), "kv")
+        assert close_frac(k, ok[layer, :pos].reshape(pos, kd)) == 1.0
+        assert close_frac(v, ov[layer, :pos].reshape(pos, kd)) == 1.0
+    m.close()

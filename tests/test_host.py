@@ -144,3 +144,38 @@ def test_quantisers_round_trip_error_bounds():
         step = amax / levels
         err = np.abs((y - x).reshape(-1, 32))
         assert np.all(err <= step * (bound + levels * 2.0 ** -11) * (1 + 1e-6))
+
+
+# ---- cross-session scheduler (host/sched.c), no device ----------------------
+@pytest.mark.parametrize("threads,steps,wait_us,device_us,host_us", [
+    (1, 40, 2000, 200, 0),      # a lone caller never waits for others
+    (8, 40, 2000, 300, 0),      # callers that return at once rejoin every batch
+    (8, 40, 0, 300, 400),       # no window, jittery host work: batches form anyway
+    (32, 20, 500, 200, 300),    # the full pool, ragged exits
+])
+def test_scheduler_rendezvous(threads, steps, wait_us, device_us, host_us):
+    """Posters on their own threads (thread i leaves after steps + i steps)
+    against a stand-in batch: every poster gets its own answer, no batch holds
+    one session twice, and concurrent posters share batches."""
+    st = np.zeros(3, np.uint64)
+    bad = native.lib().cmol__sched_selftest(threads, steps, wait_us, device_us, host_us, native.ptr(st))
+    assert bad == 0
+    batches, total, largest = (int(x) for x in st)
+    assert total == sum(steps + i for i in range(threads))
+    assert largest <= threads
+    if threads == 1:
+        assert batches == total and largest == 1
+    else:
+        assert largest > 1
+        assert batches < total
+
+
+def test_scheduler_window_gathers_returning_callers():
+    """With a window longer than the host work between steps, callers that a
+    batch releases rejoin the next one: batches stay close to the count of
+    steps of the longest-lived caller rather than one per step."""
+    threads, steps = 8, 30
+    st = np.zeros(3, np.uint64)
+    assert native.lib().cmol__sched_selftest(threads, steps, 20000, 300, 200, native.ptr(st)) == 0
+    batches = int(st[0])
+    assert batches <= steps + threads + 4
