@@ -30,8 +30,14 @@ __device__ inline float4 to_f4(const typename KVec<KT>::T &v)
 // work-group of NT threads: online softmax over chunks of CH = NT/4
 // positions.  The K and V of the next chunk are loaded while the current one
 // is reduced (K right after the scores, V right after the weighted sum).
-// Score phase: 4 threads per position, each a quarter of d_head
+// Score phase, fp32 cache: 4 threads per position, each a quarter of d_head
 // (interleaved 16-byte pieces, so a position's row is read contiguously).
+// Score phase, fp16 cache (256 threads): on MFMA.  Wave w scores positions
+// 16w..16w+15 of the chunk with v_mfma_f32_16x16x32_f16: A rows 2h, 2h+1 are
+// the high and low f16 parts of query head h (q = hi + lo/2048, exact to
+// about 22 bits, split once per split), B columns are the cached K rows as
+// stored (16-byte loads, 8 dimensions per lane), so every product is exact
+// and the sums are fp32.
 // Weighted-sum phase: thread (pg, dg) owns dims 4dg..4dg+3 and positions
 // p = pg (mod PG) of the chunk, for all G query heads.  Results leave
 // through the store policy M.
@@ -62,13 +68,24 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
     const KT *kb = (const KT *)a.kv.k_base + off;
     const KT *vb = (const KT *)a.kv.v_base + off;
 
+    // MFMA scores: fp16 cache, four waves of 16 positions per chunk
+    constexpr bool MF = sizeof(KT) == 2 && NT == 256 && CH == 64 && DH % 32 == 0;
+    constexpr int KS = MF ? DH / 32 : 1;          // MFMA k-steps per position
     const int sp_p = tid >> 2, sj = tid & 3;      // score phase
     const int dg = tid % DG, pg = tid / DG;       // weighted-sum phase
-    KV4 kr[KQ], vr[VP];
+    KV4 kr[MF ? 1 : KQ], vr[VP];
+    f16x8 km[KS];
     auto load_k = [&](int c) {
-        const int p = min(c * CH + sp_p, cnt - 1);
+        if constexpr (MF) {
+            const int p = min(c * CH + wid * 16 + (lane & 15), cnt - 1);
 #pragma unroll
-        for (int i = 0; i < KQ; i++) kr[i] = ldg((const KV4 *)(kb + (size_t)p * DH + 4 * (sj + 4 * i)));
+            for (int s = 0; s < KS; s++)
+                km[s] = ldg((const f16x8 *)(kb + (size_t)p * DH + 32 * s + 8 * (lane >> 4)));
+        } else {
+            const int p = min(c * CH + sp_p, cnt - 1);
+#pragma unroll
+            for (int i = 0; i < KQ; i++) kr[i] = ldg((const KV4 *)(kb + (size_t)p * DH + 4 * (sj + 4 * i)));
+        }
     };
     auto load_v = [&](int c) {
 #pragma unroll
@@ -88,6 +105,21 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
     __syncthreads();
 
     const float scale = 1.0f / sqrtf((float)DH);
+    // MFMA A operand: lane l feeds row l%16 (query head (l%16)/2, high or
+    // low part) with dimensions 32s + 8(l/16) .. +7 of k-step s
+    f16x8 qa[KS];
+    if constexpr (MF) {
+        const int r = lane & 15, h = r >> 1;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = h < G ? qsh[h < G ? h : 0][32 * s + 8 * (lane >> 4) + e] : 0.0f;
+                const _Float16 hi = (_Float16)x;
+                qa[s][e] = (r & 1) ? (_Float16)((x - (float)hi) * 2048.0f) : hi;
+            }
+        }
+    }
     float4 o[ATT_MAX_G];
 #pragma unroll
     for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -95,34 +127,49 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
     for (int c = 0; c < nch; c++) {
         const int ccnt = min(CH, cnt - c * CH);
         // scores of this chunk
-        float dot[ATT_MAX_G];
+        if constexpr (MF) {
+            f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int h = 0; h < ATT_MAX_G; h++) dot[h] = 0.0f;
+            for (int s = 0; s < KS; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], km[s], sc, 0, 0, 0);
+            if (c + 1 < nch) load_k(c + 1);
+            // lane l holds position 16w + l%16 for rows 4(l/16) .. +3:
+            // heads 2(l/16) and 2(l/16) + 1, high and low parts
+            const int pp = wid * 16 + (lane & 15), h0 = 2 * (lane >> 4);
 #pragma unroll
-        for (int i = 0; i < KQ; i++) {
-            const float4 kv = to_f4<KT>(kr[i]);
-            const int d0 = 4 * (sj + 4 * i);
+            for (int k = 0; k < 2; k++) {
+                const int h = h0 + k;
+                if (h < G) esh[h][pp] = pp < ccnt ? (sc[2 * k] + sc[2 * k + 1] * (1.0f / 2048.0f)) * scale : -INFINITY;
+            }
+        } else {
+            float dot[ATT_MAX_G];
 #pragma unroll
-            for (int h = 0; h < ATT_MAX_G; h++) {
-                if (h < G) {
-                    const float4 qv = *(const float4 *)&qsh[h][d0];
-                    dot[h] = fmaf(qv.x, kv.x, dot[h]);
-                    dot[h] = fmaf(qv.y, kv.y, dot[h]);
-                    dot[h] = fmaf(qv.z, kv.z, dot[h]);
-                    dot[h] = fmaf(qv.w, kv.w, dot[h]);
+            for (int h = 0; h < ATT_MAX_G; h++) dot[h] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KQ; i++) {
+                const float4 kv = to_f4<KT>(kr[i]);
+                const int d0 = 4 * (sj + 4 * i);
+#pragma unroll
+                for (int h = 0; h < ATT_MAX_G; h++) {
+                    if (h < G) {
+                        const float4 qv = *(const float4 *)&qsh[h][d0];
+                        dot[h] = fmaf(qv.x, kv.x, dot[h]);
+                        dot[h] = fmaf(qv.y, kv.y, dot[h]);
+                        dot[h] = fmaf(qv.z, kv.z, dot[h]);
+                        dot[h] = fmaf(qv.w, kv.w, dot[h]);
+                    }
                 }
             }
-        }
-        if (c + 1 < nch) load_k(c + 1);
+            if (c + 1 < nch) load_k(c + 1);
 #pragma unroll
-        for (int h = 0; h < ATT_MAX_G; h++) {
-            dot[h] += __shfl_xor(dot[h], 1, 64);
-            dot[h] += __shfl_xor(dot[h], 2, 64);
-        }
-        if (sj == 0) {
+            for (int h = 0; h < ATT_MAX_G; h++) {
+                dot[h] += __shfl_xor(dot[h], 1, 64);
+                dot[h] += __shfl_xor(dot[h], 2, 64);
+            }
+            if (sj == 0) {
 #pragma unroll
-            for (int h = 0; h < ATT_MAX_G; h++)
-                if (h < G) esh[h][sp_p] = sp_p < ccnt ? dot[h] * scale : -INFINITY;
+                for (int h = 0; h < ATT_MAX_G; h++)
+                    if (h < G) esh[h][sp_p] = sp_p < ccnt ? dot[h] * scale : -INFINITY;
+            }
         }
         __syncthreads();
         // online softmax: wave w owns heads w, w + NT/64, ...; lane j holds

@@ -197,10 +197,15 @@ def test_gemv_reference_kats(ctx):
     (15, 5, 64, [64, 1024], 64, 0), (4, 4, 128, [333], 64, 0),
     (16, 4, 128, [2304, 5, 700, 1], 256, 0), (16, 4, 128, [3000, 64, 65, 129], 192, 1),
     (9, 3, 64, [1, 17, 160, 999], 1024, 1), (4, 2, 16, [70, 3], 128, 0),
-    (8, 1, 32, [300], 64, 1), (8, 8, 256, [200, 77], 128, 0)])
+    (8, 1, 32, [300], 64, 1), (8, 8, 256, [200, 77], 128, 0),
+    # fp16 caches through the MFMA score phase: one, two, four and eight
+    # query heads per kv head, d_head 64 / 128 / 256, ragged chunk tails
+    (16, 4, 128, [4096, 1, 257, 1500], 256, 1), (4, 4, 128, [513, 64], 256, 1),
+    (8, 4, 64, [77, 700], 256, 1), (8, 8, 256, [200, 77], 128, 1), (16, 2, 128, [1000, 3], 320, 1)])
 def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16):
     """Ragged lengths across splits of one or several 64-position chunks,
-    fp32 and fp16 caches (the oracle reads the same rounded fp16 values)."""
+    fp32 and fp16 caches (the oracle reads the same rounded fp16 values; the
+    fp16 path scores on MFMA with the query split into exact f16 halves)."""
     n = len(lens)
     max_ctx = max(lens)
     rng = np.random.default_rng(n_heads * 100 + d_head + split)
