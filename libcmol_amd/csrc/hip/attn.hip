@@ -10,7 +10,10 @@
 template <int DH, typename KT>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a)
 {
-    attn_split<DH, KT, ATT_THREADS, StPlain>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+    if constexpr (sizeof(KT) == 2 && DH >= 64 && ATT_THREADS == 256)
+        attn_split_mf<DH, StPlain>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+    else
+        attn_split<DH, KT, ATT_THREADS, StPlain>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 template <int DH>

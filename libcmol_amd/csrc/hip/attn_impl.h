@@ -257,6 +257,203 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
     __syncthreads();   // the LDS areas may be reused by the caller
 }
 
+// The same split over an fp16 cache, on MFMA (a work-group of 256 threads,
+// d_head 64..256), in chunks of 64 positions:
+//   * scores: wave w takes positions 16w..16w+15 of the chunk; A rows 2h,
+//     2h+1 are the high and low f16 parts of query head h (q = hi + lo/2048),
+//     B columns the cached K rows as stored (16-byte loads), 16x16x32 f16
+//     MFMAs over d_head;
+//   * online softmax: one wave per query head; the weights e are written to
+//     LDS as exact f16 pairs (e = hi + lo/2048), the MFMA A rows of the next
+//     step;
+//   * weighted sum: wave w owns dimensions w*d_head/4 .. +d_head/4 of every
+//     head; the chunk's V rows are staged in LDS row-major (rows padded by
+//     two halves so that the eight-position column reads of the B operand
+//     fall in distinct banks) and gathered as B columns.
+// Every product is exact and every sum fp32.  Staged V is double-buffered,
+// so a chunk needs two barriers.  Same partial format as attn_split.
+template <int DH, typename M>
+__device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp, int n)
+{
+#pragma clang fp contract(off)
+    constexpr int NT = 256, CH = 64;
+    constexpr int KS = DH / 32;            // score k-steps
+    constexpr int PPP = DH / 8;            // 16-byte pieces per cached row
+    constexpr int VPT = CH * PPP / NT;     // V pieces per thread per chunk
+    constexpr int DW = DH / 4;             // dimensions per wave
+    constexpr int DTW = DW / 16;           // 16-dimension MFMA tiles per wave
+    constexpr int RS = DH + 2;             // LDS row stride of the staged V (halves)
+    static_assert(DH >= 64 && DH % 64 == 0 && VPT >= 1, "shape");
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int G = a.n_heads / a.n_kv;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int t0 = sp * a.split;
+    if (t0 >= L) return;
+    const int cnt = min(L, t0 + a.split) - t0;
+    const int nch = (cnt + CH - 1) / CH;
+    const int nact = (L + a.split - 1) / a.split;
+
+    __shared__ __attribute__((aligned(16))) float qsh[ATT_MAX_G][DH];
+    __shared__ float esh[ATT_MAX_G][CH];
+    __shared__ __attribute__((aligned(16))) _Float16 ph[2][ATT_MAX_G][CH];
+    __shared__ __attribute__((aligned(16))) _Float16 vs[2][CH * RS];
+    __shared__ float alpha_sh[ATT_MAX_G], m_sh[ATT_MAX_G], l_sh[ATT_MAX_G];
+
+    const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
+    const _Float16 *kb = (const _Float16 *)a.kv.k_base + off;
+    const _Float16 *vb = (const _Float16 *)a.kv.v_base + off;
+
+    f16x8 km[KS], vm[VPT];
+    auto load_k = [&](int c) {
+        const int p = min(c * CH + wid * 16 + (lane & 15), cnt - 1);
+#pragma unroll
+        for (int s = 0; s < KS; s++) km[s] = ldg((const f16x8 *)(kb + (size_t)p * DH + 32 * s + 8 * (lane >> 4)));
+    };
+    // piece q = tid + NT*i: position q / PPP, dimensions 8 (q % PPP) .. +7
+    auto load_v = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int q = tid + NT * i;
+            const int p = min(c * CH + q / PPP, cnt - 1);
+            vm[i] = ldg((const f16x8 *)(vb + (size_t)p * DH + 8 * (q % PPP)));
+        }
+    };
+    auto stage_v = [&](_Float16 *dst) {
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int q = tid + NT * i;
+            uint32_t *w = (uint32_t *)(dst + (q / PPP) * RS + 8 * (q % PPP));
+            const u32x4 u = __builtin_bit_cast(u32x4, vm[i]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = u[e];
+        }
+    };
+    load_k(0);
+    load_v(0);
+    const float *qn = a.q + (size_t)n * a.q_stride + (size_t)kvh * G * DH;
+    for (int i = tid; i < G * DH; i += NT) qsh[i / DH][i % DH] = *gptr(qn + i);
+    if (tid < ATT_MAX_G) {
+        m_sh[tid] = -INFINITY;
+        l_sh[tid] = 0.0f;
+        alpha_sh[tid] = 1.0f;
+    }
+    __syncthreads();
+
+    const float scale = 1.0f / sqrtf((float)DH);
+    // score A operand: lane l feeds row l%16 (query head (l%16)/2, high or
+    // low part) with dimensions 32s + 8(l/16) .. +7 of k-step s
+    const int r = lane & 15, rh = r >> 1, g = lane >> 4;
+    f16x8 qa[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float x = rh < G ? qsh[rh < G ? rh : 0][32 * s + 8 * g + e] : 0.0f;
+            const _Float16 hi = (_Float16)x;
+            qa[s][e] = (r & 1) ? (_Float16)((x - (float)hi) * 2048.0f) : hi;
+        }
+    }
+    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 oc[DTW];
+#pragma unroll
+    for (int t = 0; t < DTW; t++) oc[t] = zero4;
+    const int d0 = wid * DW + (lane & 15);   // this lane's output dimension in tile 0
+
+    for (int c = 0; c < nch; c++) {
+        const int ccnt = min(CH, cnt - c * CH);
+        _Float16 *vcur = vs[c & 1];
+        // scores of positions 16w .. 16w+15: lane l holds position 16w + l%16
+        // for rows 4(l/16) .. +3 (heads 2(l/16), 2(l/16)+1, high and low)
+        f32x4 sc = zero4;
+#pragma unroll
+        for (int s = 0; s < KS; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], km[s], sc, 0, 0, 0);
+        if (c + 1 < nch) load_k(c + 1);
+        {
+            const int pp = wid * 16 + (lane & 15);
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int h = 2 * g + k;
+                if (h < G) esh[h][pp] = pp < ccnt ? (sc[2 * k] + sc[2 * k + 1] * (1.0f / 2048.0f)) * scale : -INFINITY;
+            }
+        }
+        stage_v(vcur);
+        if (c + 1 < nch) load_v(c + 1);
+        __syncthreads();
+        // online softmax: wave w owns heads w, w + 4; lane j holds position j
+        for (int h = wid; h < G; h += NT / 64) {
+            const float sv = esh[h][lane];
+            const float mc = wave_max(sv);
+            const float mo = m_sh[h];
+            const float mn = fmaxf(mo, mc);
+            const float e = expf(sv - mn);
+            const _Float16 ehi = (_Float16)e;
+            ph[0][h][lane] = ehi;
+            ph[1][h][lane] = (_Float16)((e - (float)ehi) * 2048.0f);
+            const float ls = wave_sum(e);
+            if (lane == 0) {
+                const float al = expf(mo - mn);
+                alpha_sh[h] = al;
+                m_sh[h] = mn;
+                l_sh[h] = l_sh[h] * al + ls;
+            }
+        }
+        __syncthreads();
+        // weighted sum: rescale, then o += P . V over the chunk's 64 positions
+        {
+            const float a0 = alpha_sh[2 * g], a1 = alpha_sh[2 * g + 1];
+#pragma unroll
+            for (int t = 0; t < DTW; t++) {
+                oc[t][0] *= a0;
+                oc[t][1] *= a0;
+                oc[t][2] *= a1;
+                oc[t][3] *= a1;
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < CH / 32; ks++) {
+            const int pb = 32 * ks + 8 * g;   // this lane's eight positions
+            f16x8 pa = *(const f16x8 *)&ph[r & 1][rh < G ? rh : 0][pb];
+            if (rh >= G) pa = f16x8{};
+#pragma unroll
+            for (int t = 0; t < DTW; t++) {
+                const _Float16 *col = vcur + pb * RS + d0 + 16 * t;
+                f16x8 bv;
+#pragma unroll
+                for (int e = 0; e < 8; e++) bv[e] = col[e * RS];
+                oc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bv, oc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // outputs: lane l holds dimension d0 + 16t of heads 2(l/16) (rows 0, 1)
+    // and 2(l/16) + 1 (rows 2, 3)
+    const bool single = nact == 1;
+    const size_t sbase = (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int h = 2 * g + k;
+        if (h >= G) continue;
+#pragma unroll
+        for (int t = 0; t < DTW; t++) {
+            const int d = d0 + 16 * t;
+            const float ov = oc[t][2 * k] + oc[t][2 * k + 1] * (1.0f / 2048.0f);
+            if (single) {
+                const float fv = ov / l_sh[h];
+                const int kk = (kvh * G + h) * DH + d;
+                if (a.out) M::st(a.out + (size_t)n * a.out_stride + kk, fv);
+                if (a.next.q) act_put<M>(a.next, n, kk, fv);
+            } else {
+                M::st(a.po + (sbase + h) * DH + d, ov);
+            }
+        }
+    }
+    if (!single && tid < G) {
+        M::st(a.pm + sbase + tid, m_sh[tid]);
+        M::st(a.pl + sbase + tid, l_sh[tid]);
+    }
+    __syncthreads();   // the LDS areas may be reused by the caller
+}
+
 // Merge of the splits of one (query head, vector) by NT threads:
 // mx = max_s m_s, L = sum_s l_s e^(m_s - mx), out = sum_s o_s e^(m_s - mx) / L.
 // Thread (d, sg) sums the splits s = sg (mod SG) for dim d; the SG partial
