@@ -152,6 +152,32 @@ def bench_decode_1(path, spec, prompt_len, steps, warmup, synthetic_ctx=0):
     return out
 
 
+def bench_sampled_1(path, spec, new_tokens):
+    """One session through cmol_generate's loop with the default sampling
+    parameters (temperature 0.8, top-k 40, top-p 0.95, repeat penalty 1.1):
+    the logits of every step go to the host sampler (vocabulary 128256).
+    Timed with the sampler's worker pool and single-threaded."""
+    m = native.Model(path, max_ctx=64 + 2 * new_tokens + 8, max_sessions=1)
+    s = m.acquire()
+    prompt = synth.tokens(32, 42, spec.vocab)
+    prm = native.default_params(max_new_tokens=new_tokens, seed=5)
+    out = {}
+    L = native.lib()
+    for label, threads in (("pool", -1), ("single_thread", 0)):
+        prev = L.cmol__sampler_config(threads, 0)
+        s.reset()
+        s.generate_ids(prompt, prm, new_tokens)   # warm-up
+        s.reset()
+        t0 = time.perf_counter()
+        got = s.generate_ids(prompt, prm, new_tokens)
+        wall = time.perf_counter() - t0
+        L.cmol__sampler_config(prev, 0)
+        out[label] = {"tok_s": len(got) / wall, "tokens": int(len(got))}
+    m.close()
+    out["note"] = "wall clock includes the 32-token prompt pass"
+    return out
+
+
 def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
     lens = synth.log_uniform_lengths(sessions, lo, hi, seed=7)
     max_ctx = int(lens.max()) + warmup + steps + 8
@@ -281,7 +307,7 @@ def main():
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--generate-tokens", type=int, default=48)
-    ap.add_argument("--skip", default="", help="comma list of: decode,multi,generate,matvec,gemm,cpu")
+    ap.add_argument("--skip", default="", help="comma list of: decode,sampled,multi,generate,matvec,gemm,cpu")
     ap.add_argument("--synthetic-context", type=int, default=0,
                     help="decode after filling the KV cache with this many synthetic positions "
                          "instead of a prefill (profiling runs)")
@@ -306,6 +332,11 @@ def main():
         log("single-session decode")
         d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup, args.synthetic_context)
         log(json.dumps(d1))
+    s1 = None
+    if "sampled" not in skip:
+        log("single-session sampled generation")
+        s1 = bench_sampled_1(path, spec, args.steps)
+        log(json.dumps(s1))
     if args.copy_mb:
         log(json.dumps(copy_calibration(args.copy_mb)))
     mv = []
@@ -378,6 +409,7 @@ def main():
                    "weight_bytes_per_token": weight_bytes,
                    "effective_weight_GBps": round(weight_bytes * d1["tok_s"] / 1e9, 1)},
         "decode_1": d1,
+        "sampled_1": s1,
         "decode_32": d32,
         "generate_32": g32,
         "matvec": mv,

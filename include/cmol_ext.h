@@ -62,6 +62,14 @@ uint64_t cmol_rng_next(uint64_t state[4]);
 void cmol_apply_repeat_penalty(float *logits, int vocab_size, const int32_t *tokens,
                                int n_tokens, float penalty);
 
+/* No reference counterpart: the sampler's worker pool, which runs the
+ * element-wise parts of the softmax of vocabularies of at least min_vocab
+ * entries (default 16384) on `threads` workers (default: half the CPUs, at
+ * most 8; CMOL_SAMPLER_THREADS at first use) with bit-identical results.
+ * threads < 0 or min_vocab <= 0 keep the current value.  Returns the
+ * previous worker count. */
+int cmol__sampler_config(int threads, int min_vocab);
+
 /* Parse a GGUF and build its tokenizer only, without a device or sessions:
  * cmol_encode, cmol_decode_token and cmol_free work on the result (text-path
  * parity checks on machines without a GPU).  Same errors as cmol_load's

@@ -7,13 +7,23 @@
  * splitmix64 (src/sampler.c:37-75), so the same seed selects the same token as
  * the reference.  The repetition penalty divides positive / multiplies
  * non-positive logits, once per occurrence in the window (src/sampler.c:171-184).
+ *
+ * For large vocabularies the element-wise parts of the softmax (temperature
+ * scale, chunk maxima, expf, the final scale) run on a small pool of worker
+ * threads; the sum stays one sequential pass in index order, so every
+ * probability is bit-identical to the single-threaded computation.
  */
+#ifndef _DEFAULT_SOURCE
+#define _DEFAULT_SOURCE
+#endif
 #include "internal.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#include <unistd.h>
 
 static inline uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
 
@@ -88,6 +98,161 @@ static void softmax_inplace(float *x, int n)
     for (int i = 0; i < n; i++) x[i] *= sum;
 }
 
+/* ---- worker pool for the element-wise parts of a large softmax ---------- */
+
+#define POOL_MAX 16
+enum { PH_SCALE_MAX, PH_EXP, PH_SCALE };
+
+static struct {
+    pthread_mutex_t mu;
+    pthread_cond_t go, done;
+    pthread_once_t once;
+    int created;              /* worker threads */
+    int used;                 /* workers a softmax uses (<= created) */
+    int min_vocab;            /* smaller vocabularies run single-threaded */
+    int busy;                 /* a caller owns the pool */
+    unsigned gen;             /* job generation */
+    int left;                 /* workers still on the current job */
+    int phase, V, parts;
+    float *x, a;
+    float cmax[POOL_MAX + 1];
+} pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_ONCE_INIT,
+          0, 0, 16384, 0, 0, 0, 0, 0, 0, NULL, 0.0f, {0}};
+
+/* Part j of the current job: elements [V j / parts, V (j+1) / parts). */
+static void pool_part(int j)
+{
+    if (j >= pool.parts) return;
+    const int lo = (int)((long)pool.V * j / pool.parts), hi = (int)((long)pool.V * (j + 1) / pool.parts);
+    float *x = pool.x;
+    const float a = pool.a;
+    if (pool.phase == PH_SCALE_MAX) {
+        float m = -INFINITY;   /* NaNs never replace it, as in the sequential scan */
+        for (int i = lo; i < hi; i++) {
+            x[i] *= a;
+            if (x[i] > m) m = x[i];
+        }
+        pool.cmax[j] = m;
+    } else if (pool.phase == PH_EXP) {
+        for (int i = lo; i < hi; i++) x[i] = expf(x[i] - a);
+    } else {
+        for (int i = lo; i < hi; i++) x[i] *= a;
+    }
+}
+
+/* Spin before sleeping: the three phases of one softmax follow each other
+ * within a fraction of a millisecond, and a wake-up through the condition
+ * variable costs tens of microseconds; between two draws (a decode step) the
+ * workers sleep. */
+#define POOL_SPIN_NS 300000ull
+
+static uint64_t pool_now_ns(void)
+{
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (uint64_t)t.tv_sec * 1000000000ull + (uint64_t)t.tv_nsec;
+}
+
+static void *pool_worker(void *arg)
+{
+    const int j = (int)(intptr_t)arg;
+    unsigned seen = 0;
+    for (;;) {
+        const uint64_t t0 = pool_now_ns();
+        while (__atomic_load_n(&pool.gen, __ATOMIC_ACQUIRE) == seen && pool_now_ns() - t0 < POOL_SPIN_NS)
+            __builtin_ia32_pause();
+        pthread_mutex_lock(&pool.mu);
+        while (pool.gen == seen) pthread_cond_wait(&pool.go, &pool.mu);
+        seen = pool.gen;
+        pthread_mutex_unlock(&pool.mu);
+        pool_part(j);
+        pthread_mutex_lock(&pool.mu);
+        if (--pool.left == 0) pthread_cond_signal(&pool.done);
+        pthread_mutex_unlock(&pool.mu);
+    }
+    return NULL;
+}
+
+/* Worker count: CMOL_SAMPLER_THREADS, else half the online CPUs, at most 8. */
+static void pool_init(void)
+{
+    const char *e = getenv("CMOL_SAMPLER_THREADS");
+    long n = e ? atol(e) : sysconf(_SC_NPROCESSORS_ONLN) / 2;
+    if (!e && n > 8) n = 8;
+    if (n < 0) n = 0;
+    if (n > POOL_MAX) n = POOL_MAX;
+    int made = 0;
+    for (int j = 1; j <= n; j++) {
+        pthread_t t;
+        if (pthread_create(&t, NULL, pool_worker, (void *)(intptr_t)j) != 0) break;
+        pthread_detach(t);
+        made++;
+    }
+    pthread_mutex_lock(&pool.mu);
+    pool.created = made;
+    pool.used = made;
+    pthread_mutex_unlock(&pool.mu);
+}
+
+/* Runs one phase on the workers and the caller (part 0); pool.mu held. */
+static void pool_run(int phase, float a)
+{
+    pool.phase = phase;
+    pool.a = a;
+    pool.left = pool.created;
+    __atomic_store_n(&pool.gen, pool.gen + 1, __ATOMIC_RELEASE);
+    pthread_cond_broadcast(&pool.go);
+    pthread_mutex_unlock(&pool.mu);
+    pool_part(0);
+    const uint64_t t0 = pool_now_ns();
+    while (__atomic_load_n(&pool.left, __ATOMIC_ACQUIRE) > 0 && pool_now_ns() - t0 < POOL_SPIN_NS)
+        __builtin_ia32_pause();
+    pthread_mutex_lock(&pool.mu);
+    while (pool.left > 0) pthread_cond_wait(&pool.done, &pool.mu);
+}
+
+/* Temperature scale and softmax of x[0..V) on the pool, with the results of
+ * the sequential loops; returns 0 (nothing done) when the pool is off, busy
+ * or the vocabulary small. */
+static int pool_softmax(float *x, int V, float inv_t)
+{
+    pthread_once(&pool.once, pool_init);
+    pthread_mutex_lock(&pool.mu);
+    if (pool.busy || pool.used < 1 || V < pool.min_vocab) {
+        pthread_mutex_unlock(&pool.mu);
+        return 0;
+    }
+    pool.busy = 1;
+    pool.x = x;
+    pool.V = V;
+    pool.parts = pool.used + 1;
+    pool_run(PH_SCALE_MAX, inv_t);
+    /* the sequential scan's maximum: x[0], replaced by any greater element */
+    float mx = x[0];
+    for (int j = 0; j < pool.parts; j++)
+        if (pool.cmax[j] > mx) mx = pool.cmax[j];
+    pool_run(PH_EXP, mx);
+    pthread_mutex_unlock(&pool.mu);
+    float sum = 0.0f;
+    for (int i = 0; i < V; i++) sum += x[i];
+    pthread_mutex_lock(&pool.mu);
+    pool_run(PH_SCALE, 1.0f / sum);
+    pool.busy = 0;
+    pthread_mutex_unlock(&pool.mu);
+    return 1;
+}
+
+int cmol__sampler_config(int threads, int min_vocab)
+{
+    pthread_once(&pool.once, pool_init);
+    pthread_mutex_lock(&pool.mu);
+    const int prev = pool.used;
+    if (threads >= 0) pool.used = threads < pool.created ? threads : pool.created;
+    if (min_vocab > 0) pool.min_vocab = min_vocab;
+    pthread_mutex_unlock(&pool.mu);
+    return prev;
+}
+
 typedef struct { float p; int32_t id; } cand_t;
 #define TOPK_MAX 512
 
@@ -124,8 +289,10 @@ int32_t cmol_sample(float *logits, int V, const cmol_gen_params_t *prm, uint64_t
     if (!logits || V <= 0) return 0;
     if (!prm || prm->temperature == 0.0f) return argmax_first(logits, V);
     const float inv_t = 1.0f / prm->temperature;
-    for (int i = 0; i < V; i++) logits[i] *= inv_t;
-    softmax_inplace(logits, V);
+    if (!pool_softmax(logits, V, inv_t)) {
+        for (int i = 0; i < V; i++) logits[i] *= inv_t;
+        softmax_inplace(logits, V);
+    }
     const int use_k = prm->top_k > 0 && prm->top_k < V;
     const int use_p = prm->top_p > 0.0f && prm->top_p < 1.0f;
     if (!use_k && !use_p) {

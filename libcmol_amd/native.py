@@ -119,6 +119,7 @@ SIGNATURES = [
     ("cmol_rng_seed", None, [P, C.c_uint]),
     ("cmol_rng_next", C.c_uint64, [P]),
     ("cmol_apply_repeat_penalty", None, [P, C.c_int, P, C.c_int, C.c_float]),
+    ("cmol__sampler_config", C.c_int, [C.c_int, C.c_int]),
     ("cmol__sched_stats", C.c_int, [P, P]),
     ("cmol__sched_selftest", C.c_int, [C.c_int, C.c_int, C.c_long, C.c_long, C.c_uint, P]),
     ("cmol__session_length", C.c_int, [P]),

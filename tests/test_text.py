@@ -108,6 +108,52 @@ def test_sampler_matches_reference(ci):
     assert got == case["ids"]
 
 
+@pytest.mark.parametrize("ci", range(len(GOLD["sampler"]["cases"])))
+def test_sampler_pool_matches_reference(ci):
+    """The same reference draws with the softmax's element-wise parts on the
+    worker pool (forced on for this small vocabulary)."""
+    L = native.lib()
+    prev = L.cmol__sampler_config(4, 1)
+    try:
+        test_sampler_matches_reference(ci)
+    finally:
+        L.cmol__sampler_config(prev, 16384)
+
+
+@pytest.mark.parametrize("nan", [False, True])
+@pytest.mark.parametrize("params", [dict(), dict(top_k=0, top_p=0.9), dict(temperature=1.0, top_k=0, top_p=1.0),
+                                    dict(temperature=0.7, top_k=512, top_p=0.0)])
+def test_sampler_pool_bit_identical(params, nan):
+    """Vocabulary 128256 (SmolLM3): with and without the worker pool, the
+    same draws and bit-identical probabilities left in the logits buffer, on
+    logits with exact ties and -inf entries (and, separately, a NaN past the
+    first entry, which makes every probability NaN in both)."""
+    L, V = native.lib(), 128256
+    rng = np.random.default_rng(11)
+    base = (rng.standard_normal(V) * 4).astype(np.float32)
+    base[1000:1100] = base[5]
+    base[7::9001] = -np.inf
+    if nan:
+        base[12345] = np.nan
+    prm = native.default_params(**params)
+    out = {}
+    for threads in (0, 4):
+        prev = L.cmol__sampler_config(threads, 16384)
+        st = np.zeros(4, np.uint64)
+        L.cmol_rng_seed(st.ctypes.data, 99)
+        ids, probs = [], None
+        for d in range(6):
+            lg = np.roll(base, 1237 * d).copy()
+            ids.append(int(L.cmol_sample(lg.ctypes.data, V, prm, st.ctypes.data)))
+            probs = lg
+        L.cmol__sampler_config(prev, 16384)
+        out[threads] = (ids, probs.view(np.uint32))
+    assert out[0][0] == out[4][0]
+    assert np.array_equal(out[0][1], out[4][1])
+    if not nan:
+        assert np.isfinite(out[0][1].view(np.float32)).all() and len(set(out[0][0])) > 1
+
+
 def test_rng_stream_matches_closed_form():
     """xoshiro256** seeded by splitmix64 (src/sampler.c:37-60): the first
     outputs for seed 1 follow from the published recurrences, computed here
