@@ -693,7 +693,7 @@ static inline int gb_plan(const QTensor &w, int n, GbShape &sh)
     return sh.groups * sh.rblocks * sh.splits;
 }
 
-template <int DT, int U>
+template <int DT, int U, int EPI>
 __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
 {
 #pragma clang fp contract(off)
@@ -774,13 +774,7 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
             }
             if (sh.ss_count) y *= s_nrm[vl < nv ? vl : 0];
             const int vv = act ? v0 + vl : 0;
-            switch (sh.epi) {
-            case EPI_STORE: epilogue<EPI_STORE>(a, t, l & 15, 16, vv, act, y); break;
-            case EPI_RESID: epilogue<EPI_RESID>(a, t, l & 15, 16, vv, act, y); break;
-            case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, l & 15, 16, vv, act, y); break;
-            case EPI_QKV: epilogue<EPI_QKV>(a, t, l & 15, 16, vv, act, y); break;
-            default: epilogue<EPI_LOGITS>(a, t, l & 15, 16, vv, act, y); break;
-            }
+            epilogue<EPI>(a, t, l & 15, 16, vv, act, y);
         }
         acc = zero4;
     };
@@ -822,14 +816,25 @@ static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
     const size_t lds = (size_t)4 * sh.sq * 1024 + ((GB_VG * sh.ss_count + 3) & ~3) * 4 + GB_VG * 4;
     (void)wgs;
     constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
-    auto kern = k_gemv_b<DT, U>;
-    // kernel timing: the start event on the first kernel, the stop event on
-    // the last (the finish kernel when k is split)
-    if (a.ev_start)
-        hipExtLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GB_NW * 64), lds, s, a.ev_start,
-                              sh.splits == 1 ? a.ev_stop : nullptr, 0, a, sh);
-    else
-        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GB_NW * 64), lds, s, a, sh);
+    // the epilogue is fixed at compile time (one straight code path: a
+    // launch's cold instruction cache fetches little); with a k split the
+    // finish kernel runs it and this kernel only stores partial sums
+    auto go = [&](auto kern) {
+        // kernel timing: the start event on the first kernel, the stop event
+        // on the last (the finish kernel when k is split)
+        if (a.ev_start)
+            hipExtLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GB_NW * 64), lds, s, a.ev_start,
+                                  sh.splits == 1 ? a.ev_stop : nullptr, 0, a, sh);
+        else
+            hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GB_NW * 64), lds, s, a, sh);
+    };
+    switch (sh.splits > 1 ? EPI_STORE : epi) {
+    case EPI_STORE: go(k_gemv_b<DT, U, EPI_STORE>); break;
+    case EPI_RESID: go(k_gemv_b<DT, U, EPI_RESID>); break;
+    case EPI_SWIGLU: go(k_gemv_b<DT, U, EPI_SWIGLU>); break;
+    case EPI_QKV: go(k_gemv_b<DT, U, EPI_QKV>); break;
+    default: go(k_gemv_b<DT, U, EPI_LOGITS>); break;
+    }
     if (sh.splits > 1) return launch_gemv_b_finish(a, epi, sh.splits, sh.ss_count, s);
     return 0;
 }
