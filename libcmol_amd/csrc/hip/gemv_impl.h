@@ -654,7 +654,27 @@ static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
 #define GB_NW 8
 #define GB_VG 8
 #define GB_OP_BUDGET (64 * 1024)   // LDS bytes of one operand slice
-#define GB_TARGET_WGS 256
+// Work-groups a batched matvec aims for: fewer tiles per wave until the
+// grid reaches GB_TARGET_WGS, then k splits while it is below GB_SPLIT_WGS
+// (CMOL_GB_TARGET / CMOL_GB_SPLIT override them for measurements).
+static inline int gb_env_int(const char *name, int def)
+{
+    const char *e = getenv(name);
+    const int v = e ? atoi(e) : def;
+    return v < 1 ? 1 : v;
+}
+#define GB_TARGET_WGS gb_target_wgs()
+#define GB_SPLIT_WGS gb_split_wgs()
+static inline int gb_target_wgs()
+{
+    static const int v = gb_env_int("CMOL_GB_TARGET", 512);
+    return v;
+}
+static inline int gb_split_wgs()
+{
+    static const int v = gb_env_int("CMOL_GB_SPLIT", 256);
+    return v;
+}
 
 // Whether a matvec of n vectors over w runs the batched kernel rather than
 // k_gemv.  CMOL_GEMV_B=1 in the environment sends every unfolded matrix there.
@@ -686,7 +706,7 @@ static inline int gb_plan(const QTensor &w, int n, GbShape &sh)
     }
     sh.rblocks = (T + GB_NW * sh.tpw - 1) / (GB_NW * sh.tpw);
     // still too few work-groups: split k further
-    while (sh.groups * sh.rblocks * sh.splits < GB_TARGET_WGS && sh.sq > 1) {
+    while (sh.groups * sh.rblocks * sh.splits < GB_SPLIT_WGS && sh.sq > 1) {
         sh.sq = (sh.sq + 1) / 2;
         sh.splits = (BQ + sh.sq - 1) / sh.sq;
     }
