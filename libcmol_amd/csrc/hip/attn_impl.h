@@ -293,10 +293,14 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
     const int nch = (cnt + CH - 1) / CH;
     const int nact = (L + a.split - 1) / a.split;
 
-    __shared__ __attribute__((aligned(16))) float qsh[ATT_MAX_G][DH];
     __shared__ float esh[ATT_MAX_G][CH];
     __shared__ __attribute__((aligned(16))) _Float16 ph[2][ATT_MAX_G][CH];
     __shared__ __attribute__((aligned(16))) _Float16 vs[2][CH * RS];
+    // the query is read once, into the MFMA operand, before chunk 1 is
+    // staged: it lives in the second V buffer (LDS below 40 KB for d_head
+    // 128 keeps four work-groups on a CU)
+    static_assert(ATT_MAX_G * DH * 4 <= CH * RS * 2, "query area");
+    float *qsh = (float *)vs[1];
     __shared__ float alpha_sh[ATT_MAX_G], m_sh[ATT_MAX_G], l_sh[ATT_MAX_G];
 
     const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
@@ -331,7 +335,7 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
     load_k(0);
     load_v(0);
     const float *qn = a.q + (size_t)n * a.q_stride + (size_t)kvh * G * DH;
-    for (int i = tid; i < G * DH; i += NT) qsh[i / DH][i % DH] = *gptr(qn + i);
+    for (int i = tid; i < G * DH; i += NT) qsh[i] = *gptr(qn + i);
     if (tid < ATT_MAX_G) {
         m_sh[tid] = -INFINITY;
         l_sh[tid] = 0.0f;
@@ -348,7 +352,7 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
     for (int s = 0; s < KS; s++) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const float x = rh < G ? qsh[rh < G ? rh : 0][32 * s + 8 * g + e] : 0.0f;
+            const float x = rh < G ? qsh[(rh < G ? rh : 0) * DH + 32 * s + 8 * g + e] : 0.0f;
             const _Float16 hi = (_Float16)x;
             qa[s][e] = (r & 1) ? (_Float16)((x - (float)hi) * 2048.0f) : hi;
         }
