@@ -294,6 +294,222 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+// ---------------------------------------------------------------------------
+// Prompt-pass attention over an fp32 cache, flash style on MFMA.
+//
+// The n vectors are consecutive prompt tokens of one session (vector v at
+// position seqlen[v] - 1).  One work-group of four waves per (kv head, block
+// of QT = 64 / G tokens): its QT x G query rows (row r = token r / G, head
+// r % G) share every K/V tile.  The block walks positions 0 .. its last
+// token's position in tiles of 64:
+//   * the tile's K rows and V rows are read once and converted into f16 high
+//     and low parts in LDS (x = hi + lo / 2048), V transposed so that the
+//     weighted sum's B operand is contiguous;
+//   * wave w owns query rows 16w .. 16w+15; scores S = Q K^T come from three
+//     16x16x32 f16 MFMA products per step (hi.hi, hi.lo, lo.hi; the dropped
+//     lo.lo term is below 2^-22 of each product), scaled by 1/sqrt(d_head),
+//     positions past a row's token masked (causal);
+//   * online softmax per row (max and sum over the 16-lane groups that hold
+//     the row), the weights written to LDS as f16 high / low parts;
+//   * O += P V with the same three products per step.
+// The result goes to out / next as from attn_split.  Every product is exact
+// in fp32 and every sum fp32; the error against fp32 arithmetic is the
+// dropped low-low term.
+template <int DH>
+__global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
+{
+#pragma clang fp contract(off)
+    constexpr int TP = 64;              // positions per tile
+    constexpr int KS = DH / 32;         // MFMA k-steps over the head dimensions
+    constexpr int DT = DH / 16;         // 16-dimension output tiles
+    constexpr int KR = DH + 8;          // K row stride in LDS (halves; rows 16-byte aligned)
+    constexpr int VS = TP + 8;          // transposed V row stride (halves)
+    __shared__ __attribute__((aligned(16))) _Float16 khi[TP * KR], klo[TP * KR];
+    __shared__ __attribute__((aligned(16))) _Float16 vhi[DH * VS], vlo[DH * VS];
+    __shared__ __attribute__((aligned(16))) _Float16 pw[4][2][16][TP];
+
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, col = lane & 15;
+    const int G = a.n_heads / a.n_kv, QT = 64 / G;
+    const int kvh = blockIdx.x, vb = blockIdx.y * QT;
+    const int nt = min(QT, a.n - vb);
+    if (nt <= 0) return;
+    const int last = min(a.seqlen[(size_t)(vb + nt - 1) * a.seqlen_stride], a.max_ctx);   // positions 0 .. last-1
+    const size_t off = kv_offset(a.kv, vb) + (size_t)kvh * a.max_ctx * DH;
+    const float *kb = (const float *)a.kv.k_base + off;
+    const float *vbp = (const float *)a.kv.v_base + off;
+    const float scale = 1.0f / sqrtf((float)DH);
+
+    // A operand: lane feeds row 16w + col (token, head) with dimensions
+    // 32s + 8g .. +7 of k-step s, high and low parts
+    const int ar = 16 * wid + col, at = ar / G, ah = ar - at * G;
+    const bool arow = at < nt;
+    f16x8 qh[KS], ql[KS];
+    {
+        const float *qp = a.q + (size_t)(vb + (arow ? at : 0)) * a.q_stride + (size_t)(kvh * G + ah) * DH;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = arow ? qp[32 * s + 8 * g + e] : 0.0f;
+                const _Float16 hi = (_Float16)x;
+                qh[s][e] = hi;
+                ql[s][e] = (_Float16)((x - (float)hi) * 2048.0f);
+            }
+        }
+    }
+    // C rows of this lane: 16w + 4g + i, i = 0..3 -> (token, position limit)
+    int lim[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * wid + 4 * g + i, t = r / G;
+        lim[i] = t < nt ? min(a.seqlen[(size_t)(vb + t) * a.seqlen_stride], a.max_ctx) : 0;   // positions < lim
+    }
+    float m[4], lsum[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        m[i] = -INFINITY;
+        lsum[i] = 0.0f;
+    }
+    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 o1[DT], o2[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++) {
+        o1[t] = zero4;
+        o2[t] = zero4;
+    }
+
+    const int ntiles = (last + TP - 1) / TP;
+    for (int j = 0; j < ntiles; j++) {
+        const int p0 = j * TP;
+        // ---- stage K (row-major) and V (transposed) of positions p0 .. p0+63:
+        // lane = position, each wave a quarter of the dimensions ----
+        {
+            const int p = min(p0 + lane, last - 1);
+            const float *kr = kb + (size_t)p * DH, *vr = vbp + (size_t)p * DH;
+#pragma unroll 4
+            for (int d4 = wid; d4 < DH / 4; d4 += 4) {
+                const float4 kx = *(const float4 *)(kr + 4 * d4);
+                const float4 vx = *(const float4 *)(vr + 4 * d4);
+                const float kv[4] = {kx.x, kx.y, kx.z, kx.w}, vv[4] = {vx.x, vx.y, vx.z, vx.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const _Float16 kh = (_Float16)kv[e], vh = (_Float16)vv[e];
+                    khi[lane * KR + 4 * d4 + e] = kh;
+                    klo[lane * KR + 4 * d4 + e] = (_Float16)((kv[e] - (float)kh) * 2048.0f);
+                    vhi[(4 * d4 + e) * VS + lane] = vh;
+                    vlo[(4 * d4 + e) * VS + lane] = (_Float16)((vv[e] - (float)vh) * 2048.0f);
+                }
+            }
+        }
+        __syncthreads();
+        // ---- scores of the 64 positions (four 16-position column tiles) ----
+        float sc[4][4];   // [column tile][row i]
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            f32x4 s1 = zero4, s2 = zero4;
+            const int kp = 16 * c + col;
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+                const f16x8 bh = *(const f16x8 *)&khi[kp * KR + 32 * s + 8 * g];
+                const f16x8 bl = *(const f16x8 *)&klo[kp * KR + 32 * s + 8 * g];
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], bh, s1, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], bl, s2, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s], bh, s2, 0, 0, 0);
+            }
+            const int pos = p0 + kp;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                sc[c][i] = pos < lim[i] ? (s1[i] + s2[i] * (1.0f / 2048.0f)) * scale : -INFINITY;
+        }
+        // ---- online softmax per row: the row's 64 scores are in the 16
+        // lanes of group g, four per lane ----
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float mx = fmaxf(fmaxf(sc[0][i], sc[1][i]), fmaxf(sc[2][i], sc[3][i]));
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            const float mn = fmaxf(m[i], mx);
+            // a row with no visible position yet keeps m = -inf: weights 0
+            const float mref = mn == -INFINITY ? 0.0f : mn;
+            alpha[i] = expf(m[i] - mref);
+            float ps = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float e = expf(sc[c][i] - mref);
+                sc[c][i] = e;
+                ps += e;
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ps += __shfl_xor(ps, o, 64);
+            lsum[i] = lsum[i] * alpha[i] + ps;
+            m[i] = mn;
+        }
+        // weights to this wave's LDS rows: P[row 4g+i][position 16c+col]
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const _Float16 eh = (_Float16)sc[c][i];
+                pw[wid][0][4 * g + i][16 * c + col] = eh;
+                pw[wid][1][4 * g + i][16 * c + col] = (_Float16)((sc[c][i] - (float)eh) * 2048.0f);
+            }
+        }
+        // ---- O = alpha O + P V ----
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                o1[t][i] *= alpha[i];
+                o2[t][i] *= alpha[i];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int ks = 0; ks < TP / 32; ks++) {
+            const f16x8 ph = *(const f16x8 *)&pw[wid][0][col][32 * ks + 8 * g];
+            const f16x8 pl = *(const f16x8 *)&pw[wid][1][col][32 * ks + 8 * g];
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+                const f16x8 bh = *(const f16x8 *)&vhi[(16 * t + col) * VS + 32 * ks + 8 * g];
+                const f16x8 bl = *(const f16x8 *)&vlo[(16 * t + col) * VS + 32 * ks + 8 * g];
+                o1[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bh, o1[t], 0, 0, 0);
+                o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bl, o2[t], 0, 0, 0);
+                o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bh, o2[t], 0, 0, 0);
+            }
+        }
+        __syncthreads();   // K / V / P areas are rewritten by the next tile
+    }
+
+    // ---- outputs: lane holds rows 16w + 4g + i, dimension 16t + col ----
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * wid + 4 * g + i, t = r / G, h = r - t * G;
+        if (t >= nt) continue;
+        const int v = vb + t;
+        const float inv = 1.0f / lsum[i];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const float ov = (o1[dt][i] + o2[dt][i] * (1.0f / 2048.0f)) * inv;
+            const int k = (kvh * G + h) * DH + 16 * dt + col;
+            if (a.out) a.out[(size_t)v * a.out_stride + k] = ov;
+            if (a.next.q) act_put(a.next, v, k, ov);
+        }
+    }
+}
+
+int launch_attn_prompt(const AttnArgs &a, hipStream_t s)
+{
+    const int G = a.n_heads / a.n_kv;
+    if (a.kv_f16 || G < 1 || G > 8 || a.n_heads % a.n_kv || a.n < 1 || (a.d_head != 64 && a.d_head != 128))
+        return -4;
+    const int QT = 64 / G;
+    const dim3 grid(a.n_kv, (a.n + QT - 1) / QT), block(256);
+    if (a.d_head == 128) hipLaunchKernelGGL(k_attn_prompt<128>, grid, block, 0, s, a);
+    else hipLaunchKernelGGL(k_attn_prompt<64>, grid, block, 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int attn_max_splits(int max_ctx, int split) { return (max_ctx + split - 1) / split; }
 
 int launch_attn(const AttnArgs &a, hipStream_t s)

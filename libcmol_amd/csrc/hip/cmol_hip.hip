@@ -536,6 +536,17 @@ int pick_split(int max_ctx)
     return s;
 }
 
+// CMOL_PROMPT_ATTN=0: prompt passes use the split attention kernels
+// (measurements).
+bool prompt_attn_on()
+{
+    static const bool on = [] {
+        const char *e = getenv("CMOL_PROMPT_ATTN");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 bool is_block_fmt(int dt) { return dt == DT_Q4_0 || dt == DT_Q5_0 || dt == DT_Q8_0 || is_kquant(dt); }
 
 // Runs of consecutive q / k / v parts that share a format: run r covers
@@ -1168,7 +1179,12 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         at.po = F.po;
         at.out = nullptr;
         at.next = act_out(F.op_o, L.o.dtype, n, nullptr, nullptr, 0);
-        RC(launch_attn(at, st));
+        // the pass's tokens share every K/V tile (flash style on MFMA); other
+        // shapes and fp16 caches take the split kernels
+        if (prompt_attn_on() && launch_attn_prompt(at, st) == 0) {
+        } else {
+            RC(launch_attn(at, st));
+        }
 
         GemvArgs go{};
         go.w = to_qt(L.o);

@@ -273,6 +273,10 @@ struct AttnArgs {
 };
 
 int launch_attn(const AttnArgs &a, hipStream_t s);
+// Prompt-pass attention (flash style on MFMA) for vectors that are
+// consecutive tokens of one session over an fp32 cache, d_head 64 / 128;
+// returns -4 for shapes it does not take (the caller runs launch_attn).
+int launch_attn_prompt(const AttnArgs &a, hipStream_t s);
 
 // QK-norm models (src/attn.c:62-101): the QKV matvec stores raw q|k|v rows;
 // this stage normalises each q and k head (RMSNorm over d_head, weights
