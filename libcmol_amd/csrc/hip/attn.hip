@@ -299,9 +299,9 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 //
 // The n vectors are consecutive prompt tokens of one session (vector v at
 // position seqlen[v] - 1).  One work-group of four waves per (kv head, block
-// of QT = 64 / G tokens): its QT x G query rows (row r = token r / G, head
-// r % G) share every K/V tile.  The block walks positions 0 .. its last
-// token's position in tiles of 64:
+// of QT = 64 / G tokens, split of `split` positions): its QT x G query rows
+// (row r = token r / G, head r % G) share every K/V tile.  The work-group
+// walks its split's positions (up to its last token's) in tiles of 64:
 //   * the tile's K rows and V rows are read once and converted into f16 high
 //     and low parts in LDS (x = hi + lo / 2048), V transposed so that the
 //     weighted sum's B operand is contiguous;
@@ -312,9 +312,11 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 //   * online softmax per row (max and sum over the 16-lane groups that hold
 //     the row), the weights written to LDS as f16 high / low parts;
 //   * O += P V with the same three products per step.
-// The result goes to out / next as from attn_split.  Every product is exact
-// in fp32 and every sum fp32; the error against fp32 arithmetic is the
-// dropped low-low term.
+// A token whose positions fit one split is finished here (out / next);
+// otherwise each split leaves (max, sum of exp, unnormalised output) in the
+// partial format of attn_split and k_attn_merge combines them.  Every
+// product is exact in fp32 and every sum fp32; the error against fp32
+// arithmetic is the dropped low-low term.
 template <int DH>
 __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
 {
@@ -330,10 +332,12 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
 
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, col = lane & 15;
     const int G = a.n_heads / a.n_kv, QT = 64 / G;
-    const int kvh = blockIdx.x, vb = blockIdx.y * QT;
+    const int kvh = blockIdx.x, vb = blockIdx.y * QT, sp = blockIdx.z;
     const int nt = min(QT, a.n - vb);
     if (nt <= 0) return;
     const int last = min(a.seqlen[(size_t)(vb + nt - 1) * a.seqlen_stride], a.max_ctx);   // positions 0 .. last-1
+    const int pa = sp * a.split, pb = min(pa + a.split, last);   // this split's positions
+    if (pa >= last) return;
     const size_t off = kv_offset(a.kv, vb) + (size_t)kvh * a.max_ctx * DH;
     const float *kb = (const float *)a.kv.k_base + off;
     const float *vbp = (const float *)a.kv.v_base + off;
@@ -358,11 +362,13 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
         }
     }
     // C rows of this lane: 16w + 4g + i, i = 0..3 -> (token, position limit)
-    int lim[4];
+    int lim[4], nact[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int r = 16 * wid + 4 * g + i, t = r / G;
-        lim[i] = t < nt ? min(a.seqlen[(size_t)(vb + t) * a.seqlen_stride], a.max_ctx) : 0;   // positions < lim
+        const int L = t < nt ? min(a.seqlen[(size_t)(vb + t) * a.seqlen_stride], a.max_ctx) : 0;
+        nact[i] = (L + a.split - 1) / a.split;
+        lim[i] = min(L, pb);   // visible positions of this split: pa .. lim-1
     }
     float m[4], lsum[4];
 #pragma unroll
@@ -378,13 +384,13 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
         o2[t] = zero4;
     }
 
-    const int ntiles = (last + TP - 1) / TP;
+    const int ntiles = (pb - pa + TP - 1) / TP;
     for (int j = 0; j < ntiles; j++) {
-        const int p0 = j * TP;
+        const int p0 = pa + j * TP;
         // ---- stage K (row-major) and V (transposed) of positions p0 .. p0+63:
         // lane = position, each wave a quarter of the dimensions ----
         {
-            const int p = min(p0 + lane, last - 1);
+            const int p = min(p0 + lane, pb - 1);
             const float *kr = kb + (size_t)p * DH, *vr = vbp + (size_t)p * DH;
 #pragma unroll 4
             for (int d4 = wid; d4 < DH / 4; d4 += 4) {
@@ -485,15 +491,26 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int r = 16 * wid + 4 * g + i, t = r / G, h = r - t * G;
-        if (t >= nt) continue;
+        if (t >= nt || sp >= nact[i]) continue;   // no positions of this token here
         const int v = vb + t;
-        const float inv = 1.0f / lsum[i];
+        if (nact[i] == 1) {
+            const float inv = 1.0f / lsum[i];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const float ov = (o1[dt][i] + o2[dt][i] * (1.0f / 2048.0f)) * inv;
-            const int k = (kvh * G + h) * DH + 16 * dt + col;
-            if (a.out) a.out[(size_t)v * a.out_stride + k] = ov;
-            if (a.next.q) act_put(a.next, v, k, ov);
+            for (int dt = 0; dt < DT; dt++) {
+                const float ov = (o1[dt][i] + o2[dt][i] * (1.0f / 2048.0f)) * inv;
+                const int k = (kvh * G + h) * DH + 16 * dt + col;
+                if (a.out) a.out[(size_t)v * a.out_stride + k] = ov;
+                if (a.next.q) act_put(a.next, v, k, ov);
+            }
+        } else {
+            const size_t sb = (((size_t)v * a.n_kv + kvh) * a.max_splits + sp) * G + h;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                a.po[sb * DH + 16 * dt + col] = o1[dt][i] + o2[dt][i] * (1.0f / 2048.0f);
+            if (col == 0) {
+                a.pm[sb] = m[i];
+                a.pl[sb] = lsum[i];
+            }
         }
     }
 }
@@ -503,10 +520,15 @@ int launch_attn_prompt(const AttnArgs &a, hipStream_t s)
     const int G = a.n_heads / a.n_kv;
     if (a.kv_f16 || G < 1 || G > 8 || a.n_heads % a.n_kv || a.n < 1 || (a.d_head != 64 && a.d_head != 128))
         return -4;
+    if (a.split < 64 || a.max_splits > ATT_MAX_MERGE) return -4;
     const int QT = 64 / G;
-    const dim3 grid(a.n_kv, (a.n + QT - 1) / QT), block(256);
+    const dim3 grid(a.n_kv, (a.n + QT - 1) / QT, a.max_splits), block(256), mgrid(a.n_heads, a.n);
     if (a.d_head == 128) hipLaunchKernelGGL(k_attn_prompt<128>, grid, block, 0, s, a);
     else hipLaunchKernelGGL(k_attn_prompt<64>, grid, block, 0, s, a);
+    if (a.max_splits > 1) {
+        if (a.d_head == 128) hipLaunchKernelGGL((k_attn_merge<128>), mgrid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_attn_merge<64>), mgrid, block, 0, s, a);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -518,12 +518,36 @@ int prefill_cap(const cmolhip_hparams_t &h)
     return c < h.max_ctx ? c : h.max_ctx;
 }
 
-// Positions per attention work-group in a prompt pass: at most 16 splits.
-int prefill_split(int max_ctx)
+// CMOL_PROMPT_ATTN=0: prompt passes use the split attention kernels
+// (measurements).
+bool prompt_attn_on()
 {
-    int s = (max_ctx + 15) / 16;
+    static const bool on = [] {
+        const char *e = getenv("CMOL_PROMPT_ATTN");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// Whether prompt passes of this model run the flash-style prompt attention
+// (fp32 cache, d_head 64 / 128, at most 8 query heads per kv head).
+bool prompt_attn_fits(const cmolhip_hparams_t &h)
+{
+    const int G = h.n_heads / h.n_kv_heads;
+    return prompt_attn_on() && !h.kv_f16 && (h.d_head == 64 || h.d_head == 128) && G >= 1 && G <= 8;
+}
+
+// Positions per attention work-group in a prompt pass: the split kernels
+// take at most 16 splits of at least 1024 positions; the prompt kernel, whose
+// work-groups already share K/V across 64 query rows, at most 32 splits of
+// at least 256 (more work-groups for a pass over a short prefix).
+int prefill_split(const cmolhip_hparams_t &h)
+{
+    const bool pk = prompt_attn_fits(h);
+    int s = (h.max_ctx + (pk ? 31 : 15)) / (pk ? 32 : 16);
     s = (s + 63) / 64 * 64;
-    return s < 1024 ? 1024 : s;
+    const int lo = pk ? 256 : 1024;
+    return s < lo ? lo : s;
 }
 
 int pick_split(int max_ctx)
@@ -534,17 +558,6 @@ int pick_split(int max_ctx)
     if (s < ATTN_SPLIT_MIN) s = ATTN_SPLIT_MIN;
     if (s > ATTN_SPLIT_MAX) s = ATTN_SPLIT_MAX;
     return s;
-}
-
-// CMOL_PROMPT_ATTN=0: prompt passes use the split attention kernels
-// (measurements).
-bool prompt_attn_on()
-{
-    static const bool on = [] {
-        const char *e = getenv("CMOL_PROMPT_ATTN");
-        return !(e && e[0] == '0');
-    }();
-    return on;
 }
 
 bool is_block_fmt(int dt) { return dt == DT_Q4_0 || dt == DT_Q5_0 || dt == DT_Q8_0 || is_kquant(dt); }
@@ -790,7 +803,7 @@ void plan_prefill(Plan &P, const cmolhip_model_desc_t *d)
 {
     const cmolhip_hparams_t &h = d->hp;
     const int cap = prefill_cap(h);
-    const int ms = attn_max_splits(h.max_ctx, prefill_split(h.max_ctx));
+    const int ms = attn_max_splits(h.max_ctx, prefill_split(h));
     const size_t np = (size_t)h.n_kv_heads * ms * (h.n_heads / h.n_kv_heads);
     P.add((size_t)cap * 3 * 4);
     P.add((size_t)cap * 4);
@@ -1287,7 +1300,7 @@ int build_prefill(cmolhip_model *m, Prefill &F)
     cmolhip_ctx_t *c = m->ctx;
     const cmolhip_hparams_t &h = m->hp;
     F.cap = prefill_cap(h);
-    F.split = prefill_split(h.max_ctx);
+    F.split = prefill_split(h);
     F.max_splits = attn_max_splits(h.max_ctx, F.split);
     const int cap = F.cap;
     const size_t np = (size_t)h.n_kv_heads * F.max_splits * (h.n_heads / h.n_kv_heads);
