@@ -273,3 +273,36 @@ def test_short_prompts_match_oracle(gpu, model_dir, preset, sessions):
         assert close_frac(k, ok[layer, :pos].reshape(pos, kd)) == 1.0
         assert close_frac(v, ov[layer, :pos].reshape(pos, kd)) == 1.0
     m.close()
+
+
+@pytest.mark.parametrize("heads,kv,d_model", [(4, 1, 512), (8, 1, 512), (2, 2, 256), (16, 4, 1024)])
+@pytest.mark.parametrize("chunk", [128, 512])
+def test_prompt_attention_shapes_match_oracle(gpu, model_dir, heads, kv, d_model, chunk):
+    """The flash-style prompt attention for 1, 2, 4 and 8 query heads per kv
+    head at d_head 64 and 128: a 300-token prompt in passes of 128 tokens (the
+    later passes attend to the cache the earlier ones wrote) or in one pass
+    (positions beyond one 256-position split, merged): logits after the
+    prompt and the whole KV cache match the oracle's token-by-token forward."""
+    spec = synth.ModelSpec(2, d_model, heads, kv, 2 * d_model, 1024, ctx_len=512, wtype=synth.Q8_0,
+                           embd_type=synth.Q8_0, wstd=0.08, seed=heads * 10 + kv)
+    path = synth.model_file(spec, model_dir)
+    prompt = synth.tokens(300, 31, spec.vocab)
+    m = native.Model(path, max_ctx=320, max_sessions=1, prefill_chunk=chunk)
+    s = m.acquire()
+    am, lg = s.prefill(prompt, spec.vocab)
+    om = O.Model(path, 320)
+    for p, t in enumerate(prompt):
+        want = om.forward(int(t), p)
+    assert close_frac(lg, want) == 1.0
+    assert am == int(np.argmax(want))
+    ok, ov = om.kv()
+    kd = spec.n_kv_heads * spec.d_head
+    n = len(prompt)
+    for layer in range(spec.n_layers):
+        k = np.zeros((n, kd), np.float32)
+        v = np.zeros((n, kd), np.float32)
+        native.check(native.lib().cmolhip_kv_download(m.device, s.slot, layer, n,
+                                                       native.ptr(k), native.ptr(v)), "kv")
+        assert close_frac(k, ok[layer, :n].reshape(n, kd)) == 1.0
+        assert close_frac(v, ov[layer, :n].reshape(n, kd)) == 1.0
+    m.close()
