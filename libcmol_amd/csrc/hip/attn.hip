@@ -318,10 +318,11 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 // product is exact in fp32 and every sum fp32; the error against fp32
 // arithmetic is the dropped low-low term.
 template <int DH>
-__global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_prompt(AttnArgs a)
 {
 #pragma clang fp contract(off)
-    constexpr int TP = 64;              // positions per tile
+    constexpr int TP = 32;              // positions per tile (LDS for two work-groups per CU)
+    constexpr int NDG = 256 / TP;       // staging threads per position
     constexpr int KS = DH / 32;         // MFMA k-steps over the head dimensions
     constexpr int DT = DH / 16;         // 16-dimension output tiles
     constexpr int KR = DH + 8;          // K row stride in LDS (halves; rows 16-byte aligned)
@@ -387,31 +388,34 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
     const int ntiles = (pb - pa + TP - 1) / TP;
     for (int j = 0; j < ntiles; j++) {
         const int p0 = pa + j * TP;
-        // ---- stage K (row-major) and V (transposed) of positions p0 .. p0+63:
-        // lane = position, each wave a quarter of the dimensions ----
+        // ---- stage K (row-major) and V (transposed) of positions p0 ..
+        // p0+TP-1: thread = (position tid % TP, dimension quads tid / TP +
+        // NDG k) ----
         {
-            const int p = min(p0 + lane, pb - 1);
+            const int pl = tid % TP, dg = tid / TP;
+            const int p = min(p0 + pl, pb - 1);
             const float *kr = kb + (size_t)p * DH, *vr = vbp + (size_t)p * DH;
 #pragma unroll 4
-            for (int d4 = wid; d4 < DH / 4; d4 += 4) {
+            for (int d4 = dg; d4 < DH / 4; d4 += NDG) {
                 const float4 kx = *(const float4 *)(kr + 4 * d4);
                 const float4 vx = *(const float4 *)(vr + 4 * d4);
                 const float kv[4] = {kx.x, kx.y, kx.z, kx.w}, vv[4] = {vx.x, vx.y, vx.z, vx.w};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const _Float16 kh = (_Float16)kv[e], vh = (_Float16)vv[e];
-                    khi[lane * KR + 4 * d4 + e] = kh;
-                    klo[lane * KR + 4 * d4 + e] = (_Float16)((kv[e] - (float)kh) * 2048.0f);
-                    vhi[(4 * d4 + e) * VS + lane] = vh;
-                    vlo[(4 * d4 + e) * VS + lane] = (_Float16)((vv[e] - (float)vh) * 2048.0f);
+                    khi[pl * KR + 4 * d4 + e] = kh;
+                    klo[pl * KR + 4 * d4 + e] = (_Float16)((kv[e] - (float)kh) * 2048.0f);
+                    vhi[(4 * d4 + e) * VS + pl] = vh;
+                    vlo[(4 * d4 + e) * VS + pl] = (_Float16)((vv[e] - (float)vh) * 2048.0f);
                 }
             }
         }
         __syncthreads();
-        // ---- scores of the 64 positions (four 16-position column tiles) ----
-        float sc[4][4];   // [column tile][row i]
+        // ---- scores of the tile's positions (16-position column tiles) ----
+        constexpr int NC = TP / 16;
+        float sc[NC][4];   // [column tile][row i]
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < NC; c++) {
             f32x4 s1 = zero4, s2 = zero4;
             const int kp = 16 * c + col;
 #pragma unroll
@@ -427,12 +431,14 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
             for (int i = 0; i < 4; i++)
                 sc[c][i] = pos < lim[i] ? (s1[i] + s2[i] * (1.0f / 2048.0f)) * scale : -INFINITY;
         }
-        // ---- online softmax per row: the row's 64 scores are in the 16
-        // lanes of group g, four per lane ----
+        // ---- online softmax per row: the row's scores are in the 16 lanes
+        // of group g, NC per lane ----
         float alpha[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            float mx = fmaxf(fmaxf(sc[0][i], sc[1][i]), fmaxf(sc[2][i], sc[3][i]));
+            float mx = sc[0][i];
+#pragma unroll
+            for (int c = 1; c < NC; c++) mx = fmaxf(mx, sc[c][i]);
 #pragma unroll
             for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
             const float mn = fmaxf(m[i], mx);
@@ -441,7 +447,7 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
             alpha[i] = expf(m[i] - mref);
             float ps = 0.0f;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
+            for (int c = 0; c < NC; c++) {
                 const float e = expf(sc[c][i] - mref);
                 sc[c][i] = e;
                 ps += e;
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(256) void k_attn_prompt(AttnArgs a)
         }
         // weights to this wave's LDS rows: P[row 4g+i][position 16c+col]
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < NC; c++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const _Float16 eh = (_Float16)sc[c][i];
