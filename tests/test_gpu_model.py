@@ -306,3 +306,30 @@ def test_prompt_attention_shapes_match_oracle(gpu, model_dir, heads, kv, d_model
         assert close_frac(k, ok[layer, :n].reshape(n, kd)) == 1.0
         assert close_frac(v, ov[layer, :n].reshape(n, kd)) == 1.0
     m.close()
+
+
+def test_smollm3_3b_shape_matches_oracle(gpu, model_dir):
+    """The benchmarked shape itself (SmolLM3-3B: 36 layers, hidden 2048,
+    16/4 heads of 128, FFN 11008, vocab 128256, Q4_0 with a Q8_0 tied
+    embedding; NoPE every 4th layer), weights at 2.5x the preset's scale for
+    a varied continuation: logits after a 20-token prompt (prompt GEMMs,
+    flash-style prompt attention) and 6 greedy tokens (decode graph) match
+    the oracle.  After 36 layers of fp32 sums in another order the logits
+    are held to 1e-3 relative plus an absolute 1e-4 of the largest logit
+    (the per-kernel 1e-4 absolute floor is in units of the kernel outputs;
+    measured: at most 2.2e-4 absolute on logits of spread 2.3)."""
+    spec = synth.PRESETS["smollm3-3b-q4_0"].replace(wstd=0.05)
+    path = synth.model_file(spec, model_dir)
+    prompt = synth.tokens(20, 77, spec.vocab)
+    m = native.Model(path, max_ctx=64, max_sessions=1)
+    s = m.acquire()
+    am, lg = s.prefill(prompt, spec.vocab)
+    om = O.Model(path, 64)
+    for p, t in enumerate(prompt):
+        want = om.forward(int(t), p)
+    assert close_frac(lg, want, atol=1e-4 * float(np.abs(want).max())) == 1.0
+    assert am == int(np.argmax(want))
+    s.reset()
+    got = s.generate_ids(prompt, native.greedy_params(6), 6)
+    m.close()
+    assert got.tolist() == O.Model(path, 64).generate(prompt, 6).tolist()
