@@ -1,4 +1,4 @@
-"""Text path against the reference (§8(f) first row): tokenizer encode and
+"""Text path against the reference: tokenizer encode and
 decode, the sampler, and cmol_generate on text prompts.
 
 Every expected value in tests/golden/text_golden.json was produced by the
