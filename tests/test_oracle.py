@@ -172,6 +172,21 @@ def test_yarn_key_is_not_applied(model_dir):
     assert O.Model(plain, 128).generate(prompt, 40).tolist() == QN["qkn_smollm3_yarn_ids"].tolist()
 
 
+# ---- generate-loop stop rules (tests/golden/make_generate_golden.py) --------
+GE = np.load(os.path.join(HERE, "golden", "generate_edges.npz"))
+
+
+def test_generate_stop_rules_match_reference(model_dir):
+    """The oracle's greedy loop stops as the reference's: after emitting the
+    EOS id, and after the token sampled at the last context position."""
+    from tests.golden import make_generate_golden as ge
+    prompt = GE["prompt"]
+    path = synth.model_file(ge.eos_spec(int(GE["eos_id"][0])), model_dir)
+    assert O.Model(path, 128).generate(prompt, 40).tolist() == GE["eos_ids"].tolist()
+    path = synth.model_file(ge.eos_spec(), model_dir)
+    assert O.Model(path, ge.CTX_FULL).generate(prompt, 64).tolist() == GE["ctx_full_ids"].tolist()
+
+
 def test_q4_k_closed_form():
     """Q4_K: sub-block j of a super-block with d = 1, dmin = 0.5, scale
     j + 1 and min 2j (the six-bit packing spelled out by hand, bits 4-5 of
