@@ -506,7 +506,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
 
 static inline int pick_nw(int tiles, int quads)
 {
-    int nw = tiles < 128 ? 16 : 8;
+    int nw = tiles < 128 ? 16 : tiles < 4096 ? 8 : 4;
     if (const char *e = getenv("CMOL_GEMV_NW")) nw = atoi(e);
     while (nw > 1 && quads < 2 * nw) nw >>= 1;
     return nw;
