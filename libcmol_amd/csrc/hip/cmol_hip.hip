@@ -605,7 +605,8 @@ void add_q(Plan &P, int dt, int rows, int cols, int fold)
 }
 
 // k parts per tile for a projection: single-session models fold matrices
-// with few rows until they make >= 256 work-groups at batch 1, as long as
+// with few rows until they make >= 192 row tiles at batch 1 (CMOL_FOLD_TILES
+// overrides the target for measurements), as long as
 // the parts stay whole quads (padding <= 1/16); batched models keep fold 1,
 // whose tiles serve up to 8 vectors per MFMA.
 int pick_fold(int rows, int cols, int max_sessions)
@@ -613,7 +614,12 @@ int pick_fold(int rows, int cols, int max_sessions)
     if (max_sessions > 1) return 1;
     const int nb = cols / 32;
     int f = 1;
-    while (f < 8 && (rows + 16 / f - 1) / (16 / f) < 256) {
+    static const int target = [] {
+        const char *e = getenv("CMOL_FOLD_TILES");   // measurements
+        const int v = e ? atoi(e) : 192;
+        return v < 1 ? 1 : v;
+    }();
+    while (f < 8 && (rows + 16 / f - 1) / (16 / f) < target) {
         const int nf = 2 * f;
         if (nf * fold_quads(nb, nf) * 4 > nb + nb / 16) break;
         f = nf;
