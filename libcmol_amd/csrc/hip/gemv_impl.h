@@ -508,7 +508,12 @@ static inline int pick_nw(int tiles, int quads)
 {
     int nw = tiles < 128 ? 16 : tiles < 4096 ? 8 : 4;
     if (const char *e = getenv("CMOL_GEMV_NW")) nw = atoi(e);
-    while (nw > 1 && quads < 2 * nw) nw >>= 1;
+    static const int minq = [] {
+        const char *e = getenv("CMOL_GEMV_MINQ");   // measurements
+        const int v = e ? atoi(e) : 2;
+        return v < 1 ? 1 : v;
+    }();
+    while (nw > 1 && quads < minq * nw) nw >>= 1;
     return nw;
 }
 
