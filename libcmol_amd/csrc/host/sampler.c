@@ -307,17 +307,31 @@ int32_t cmol_sample(float *logits, int V, const cmol_gen_params_t *prm, uint64_t
     cand_t heap[TOPK_MAX];
     int k = use_k ? prm->top_k : V;
     if (k > TOPK_MAX) k = TOPK_MAX;
-    int n = 0;
-    for (int i = 0; i < V; i++) {
-        if (n < k) {
-            heap[n].p = logits[i];
-            heap[n].id = i;
-            heap_up(heap, n++);
-        } else if (logits[i] > heap[0].p) {
+    int n = 0, i = 0;
+    for (; i < V && n < k; i++) {
+        heap[n].p = logits[i];
+        heap[n].id = i;
+        heap_up(heap, n++);
+    }
+    /* The same in-order scan, but a run of 16 elements none of which beats
+     * the heap's minimum (NaN never does) is passed over in one vector
+     * compare: the minimum only changes on a hit, so the heap ends the same. */
+    while (i < V) {
+        if (i + 16 <= V) {
+            const float h = heap[0].p;
+            int any = 0;
+            for (int j = 0; j < 16; j++) any |= logits[i + j] > h;
+            if (!any) {
+                i += 16;
+                continue;
+            }
+        }
+        if (logits[i] > heap[0].p) {
             heap[0].p = logits[i];
             heap[0].id = i;
             heap_down(heap, 0, k);
         }
+        i++;
     }
     qsort(heap, (size_t)n, sizeof(cand_t), by_p_desc);
     int nuc = n;

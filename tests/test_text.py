@@ -9,6 +9,7 @@ cmol_rng_seed and cmol_apply_repeat_penalty, and cmol_generate's sampled ids.
 The fixture carries the tokenizers, so the GGUFs are rebuilt here with the
 synthetic-model writer.  Tokenizer and sampler checks run on the CPU (the
 text-only load needs no device); generation runs on the GPU."""
+import ctypes as C
 import json
 import os
 
@@ -17,6 +18,7 @@ import pytest
 
 import libcmol_amd.native as native
 from libcmol_amd import synth
+from oracle import oracle as O
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLD = json.load(open(os.path.join(HERE, "golden", "text_golden.json")))
@@ -203,3 +205,30 @@ def test_generate_text_matches_reference(gpu, text_dir, name):
         assert rc == 0
         assert [p for p, _ in got] == [pieces[i] for i in case["ids"]], case["prompt"]
     m.close()
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference library not built")
+@pytest.mark.parametrize("k,p", [(40, 0.95), (512, 0.0), (7, 1.0)])
+def test_sampler_top_k_matches_reference_full_vocab(k, p):
+    """Vocabulary 128256: the top-k scan (which passes over runs of entries
+    that cannot enter the heap) keeps the reference heap's order, checked on
+    logits whose largest values are exact ties (so the draw depends on the
+    heap's arrangement), over 16 seeded draws against the reference library
+    built from its sources (src/sampler.c:171-268)."""
+    L, R, V = native.lib(), O.ref(), 128256
+    R.cmol_sample.restype = C.c_int32
+    R.cmol_rng_seed.restype = None
+    prm = native.default_params(temperature=0.8, top_k=k, top_p=p)
+    rng = np.random.default_rng(5)
+    st_a, st_b = np.zeros(4, np.uint64), np.zeros(4, np.uint64)
+    L.cmol_rng_seed(st_a.ctypes.data, 77)
+    R.cmol_rng_seed(C.c_void_p(st_b.ctypes.data), C.c_uint(77))
+    for d in range(16):
+        x = (rng.standard_normal(V) * 3).astype(np.float32)
+        top = np.sort(x)[-3 * k:]
+        x[rng.choice(V, 2 * k, replace=False)] = top[rng.integers(0, 4, 2 * k)]   # ties near the top
+        a, b = x.copy(), x.copy()
+        ia = L.cmol_sample(a.ctypes.data, V, prm, st_a.ctypes.data)
+        ib = R.cmol_sample(C.c_void_p(b.ctypes.data), C.c_int(V), C.byref(prm), C.c_void_p(st_b.ctypes.data))
+        assert ia == ib, f"draw {d}"
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"draw {d}"
