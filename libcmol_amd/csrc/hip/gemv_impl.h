@@ -504,9 +504,18 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
     }
 }
 
+// positive integer from the environment, else def
+static inline int gb_env_int(const char *name, int def)
+{
+    const char *e = getenv(name);
+    const int v = e ? atoi(e) : def;
+    return v < 1 ? 1 : v;
+}
+
 static inline int pick_nw(int tiles, int quads)
 {
-    int nw = tiles < 128 ? 16 : tiles < 4096 ? 8 : 4;
+    static const int t16 = gb_env_int("CMOL_NW16_BELOW", 128), t8 = gb_env_int("CMOL_NW8_BELOW", 4096);   // measurements
+    int nw = tiles < t16 ? 16 : tiles < t8 ? 8 : 4;
     if (const char *e = getenv("CMOL_GEMV_NW")) nw = atoi(e);
     static const int minq = [] {
         const char *e = getenv("CMOL_GEMV_MINQ");   // measurements
@@ -662,12 +671,6 @@ static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
 // Work-groups a batched matvec aims for: fewer tiles per wave until the
 // grid reaches GB_TARGET_WGS, then k splits while it is below GB_SPLIT_WGS
 // (CMOL_GB_TARGET / CMOL_GB_SPLIT override them for measurements).
-static inline int gb_env_int(const char *name, int def)
-{
-    const char *e = getenv(name);
-    const int v = e ? atoi(e) : def;
-    return v < 1 ? 1 : v;
-}
 #define GB_TARGET_WGS gb_target_wgs()
 #define GB_SPLIT_WGS gb_split_wgs()
 static inline int gb_target_wgs()
