@@ -64,11 +64,17 @@ void cmol_apply_repeat_penalty(float *logits, int vocab_size, const int32_t *tok
 
 /* No reference counterpart: the sampler's worker pool, which runs the
  * element-wise parts of the softmax of vocabularies of at least min_vocab
- * entries (default 16384) on `threads` workers (default: half the CPUs, at
- * most 8; CMOL_SAMPLER_THREADS at first use) with bit-identical results.
- * threads < 0 or min_vocab <= 0 keep the current value.  Returns the
- * previous worker count. */
+ * entries (default 16384) on worker threads with bit-identical results.
+ * The pool exists while a model is loaded: cmol_load starts it and the last
+ * cmol_free joins its threads.  cmol__sampler_config sets the workers a
+ * softmax uses (at most the pool's; before the first start, the pool's size,
+ * else CMOL_SAMPLER_THREADS or half the CPUs, at most 8) and min_vocab;
+ * threads < 0 or min_vocab <= 0 keep the current value; returns the previous
+ * worker count.  cmol__sampler_pool(1) holds the pool as a load does and
+ * cmol__sampler_pool(0) releases that hold (sampler checks without a model);
+ * it returns the pool's worker count after the call. */
 int cmol__sampler_config(int threads, int min_vocab);
+int cmol__sampler_pool(int on);
 
 /* Parse a GGUF and build its tokenizer only, without a device or sessions:
  * cmol_encode, cmol_decode_token and cmol_free work on the result (text-path

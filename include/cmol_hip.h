@@ -157,6 +157,19 @@ typedef struct {
 
 /* Validate the description and report the device arena it needs. */
 int cmolhip_model_plan(const cmolhip_model_desc_t *desc, size_t *device_bytes);
+/* Launch planning, without a device.  The batched matvec (9..32 vectors)
+ * may split k over work-groups and keep partial sums in a scratch buffer:
+ * cmolhip_gemv_scratch_floats gives the floats one launch over a rows x
+ * cols tensor (dtype, fold) of n vectors needs (0: no split, or a shape it
+ * does not run); cmolhip_batch_scratch_floats the scratch a model reserves
+ * for a batch of up to cap vectors (the largest need of any launch of a
+ * decode step of 1..cap vectors; q, k and v launch once per run of parts
+ * that share a format).  A launch whose need exceeds the scratch it is
+ * given is refused with CMOL_ERR_ARGS.  These replace no reference
+ * interface: the reference's n > 1 matvec (src/quant.c:546-553) needs no
+ * scratch. */
+size_t cmolhip_gemv_scratch_floats(int dtype, int rows, int cols, int fold, int n);
+int cmolhip_batch_scratch_floats(const cmolhip_model_desc_t *desc, int cap, size_t *floats);
 /* Allocate the arena once, upload every tensor, create per-session streams
  * and capture each session's decode graph.  Nothing is allocated later. */
 int cmolhip_model_create(const cmolhip_model_desc_t *desc, int device,

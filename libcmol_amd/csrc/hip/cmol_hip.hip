@@ -333,6 +333,7 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
     int rc = E_OK;
     const size_t pf = n <= 32 ? gemv_part_floats(a.w, n) : 0;
     if (pf) rc = arena_get(c, pf, &a.part);
+    a.part_cap = pf;
     if (rc == E_OK) rc = n <= 32 ? launch_gemv(a, EPI_STORE, c->stream) : launch_gemm(a, EPI_STORE, c->stream);
     arena_release(c, mark);
     return rc;
@@ -369,21 +370,21 @@ int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float
         float *dx = nullptr, *dy = nullptr;
         cmolhip_qtensor_t t{};
         if ((rc = cmolhip_alloc(c, rb * (size_t)m, ALIGN, &staging))) break;
-        if ((rc = arena_get(c, (size_t)k * n, &dx))) break;
-        if ((rc = arena_get(c, (size_t)m * n, &dy))) break;
+        const size_t big = (size_t)(k > m ? k : m) * n;   // each buffer holds either side
+        if ((rc = arena_get(c, big, &dx))) break;
+        if ((rc = arena_get(c, big, &dy))) break;
         const void *parts[1] = {a};
         const int32_t rows[1] = {m};
         if ((rc = cmolhip_qtensor_upload(c, dtype, k, 1, 1, parts, rows, CMOLHIP_PARTS_CONCAT, staging,
                                          rb * (size_t)m, &t)))
             break;
-        std::vector<float> xt((size_t)k * n), yt((size_t)m * n);
-        for (int ki = 0; ki < k; ki++)
-            for (int ni = 0; ni < n; ni++) xt[(size_t)ni * k + ki] = b[(size_t)ki * n + ni];
-        if ((rc = cmolhip_memcpy_h2d(c, dx, xt.data(), xt.size() * 4))) break;
+        // B[k][n] -> x[n][k] and y[n][m] -> out[m][n] on the device: the
+        // call allocates no host memory
+        if ((rc = cmolhip_memcpy_h2d(c, dy, b, (size_t)k * n * 4))) break;
+        if ((rc = launch_transpose(dy, dx, k, n, c->stream))) break;
         if ((rc = cmolhip_gemm(c, &t, dx, dy, n, nullptr, 0.0f))) break;
-        if ((rc = cmolhip_memcpy_d2h(c, yt.data(), dy, yt.size() * 4))) break;
-        for (int mi = 0; mi < m; mi++)
-            for (int ni = 0; ni < n; ni++) out[(size_t)mi * n + ni] = yt[(size_t)ni * m + mi];
+        if ((rc = launch_transpose(dy, dx, n, m, c->stream))) break;
+        if ((rc = cmolhip_memcpy_d2h(c, out, dx, (size_t)m * n * 4))) break;
     } while (0);
     arena_release(c, mark);
     return rc;
@@ -407,9 +408,7 @@ int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kca
         if ((rc = arena_get(c, np, &pm)) || (rc = arena_get(c, np, &pl)) ||
             (rc = arena_get(c, np * d_head, &po)) || (rc = arena_get(c, (size_t)n, &ids)))
             break;
-        std::vector<int32_t> hid(n);
-        for (int i = 0; i < n; i++) hid[i] = i;
-        if ((rc = cmolhip_memcpy_h2d(c, ids, hid.data(), (size_t)n * 4))) break;
+        if ((rc = launch_iota(ids, n, c->stream))) break;   // cache i belongs to session i
         AttnArgs a{};
         a.q = q;
         a.q_stride = n_heads * d_head;
@@ -471,6 +470,7 @@ struct Batch {
     unsigned long long *argmax = nullptr;     // [cap][ARGMAX_SLOTS]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
     float *part = nullptr;                    // k-split partial sums of batched matvecs
+    size_t part_cap = 0;                      // floats at part
     float *qkv_raw = nullptr;                 // QK-norm models: [cap][d + 2 kvd] q|k|v rows
     int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
@@ -563,24 +563,34 @@ int pick_split(int max_ctx)
 bool is_block_fmt(int dt) { return dt == DT_Q4_0 || dt == DT_Q5_0 || dt == DT_Q8_0 || is_kquant(dt); }
 
 // Runs of consecutive q / k / v parts that share a format: run r covers
-// parts first[r] .. first[r] + count[r] - 1 (rows of q, k, v: d, kvd, kvd).
-int qkv_runs(const cmolhip_layer_tensors_t &L, int first[3], int count[3])
+// parts first[r] .. first[r] + count[r] - 1 (rows of q, k, v: d, kvd, kvd),
+// rows[r] output rows of format dt[r].  Each run is one uploaded tensor and
+// one matvec launch per stage, so the arena plan, the upload and the k-split
+// scratch all read their shapes from here.
+struct QkvRuns {
+    int n = 0;
+    int first[3]{}, count[3]{}, rows[3]{}, dt[3]{};
+};
+
+QkvRuns qkv_runs(const cmolhip_layer_tensors_t &L, const cmolhip_hparams_t &h)
 {
     const int dt[3] = {L.q.dtype, L.k.dtype, L.v.dtype};
-    int n = 0;
+    const int rows[3] = {h.d_model, h.n_kv_heads * h.d_head, h.n_kv_heads * h.d_head};
+    QkvRuns R;
     for (int p = 0; p < 3; p++) {
-        if (n && dt[p] == dt[first[n - 1]]) {
-            count[n - 1]++;
+        if (R.n && dt[p] == R.dt[R.n - 1]) {
+            R.count[R.n - 1]++;
+            R.rows[R.n - 1] += rows[p];
         } else {
-            first[n] = p;
-            count[n] = 1;
-            n++;
+            R.first[R.n] = p;
+            R.count[R.n] = 1;
+            R.rows[R.n] = rows[p];
+            R.dt[R.n] = dt[p];
+            R.n++;
         }
     }
-    return n;
+    return R;
 }
-
-int qkv_part_rows(const cmolhip_hparams_t &h, int p) { return p == 0 ? h.d_model : h.n_kv_heads * h.d_head; }
 
 // Byte sizes of everything the model puts in the arena, in creation order.
 struct Plan {
@@ -749,31 +759,45 @@ QTensor shape_qt(int dt, int rows, int cols, int fold)
     return t;
 }
 
-// Largest k-split scratch any matvec of a batch of up to cap vectors of
-// model d needs (the split count depends on the batch size).
-size_t batch_part_floats(const cmolhip_model_desc_t *d, int cap)
+// Every matvec launch of one decode step of model d, in launch order:
+// f(dtype, rows, cols, fold).  q|k|v launch once per run of formats
+// (enqueue_step, enqueue_qk_norm).
+template <class F>
+void for_each_step_matvec(const cmolhip_model_desc_t *d, F f)
 {
     const cmolhip_hparams_t &h = d->hp;
-    const int kvd = h.n_kv_heads * h.d_head;
-    size_t m = 0;
-    auto upd = [&](int dt, int rows, int cols) {
-        const QTensor t = shape_qt(dt, rows, cols, layer_fold(d, rows, cols));
-        for (int n = 1; n <= cap; n++) {
-            const size_t f = gemv_part_floats(t, n);
-            m = f > m ? f : m;
-        }
-    };
     for (int l = 0; l < h.n_layers; l++) {
         const cmolhip_layer_tensors_t &L = d->layers[l];
-        upd(L.q.dtype, h.d_model + 2 * kvd, h.d_model);
-        upd(L.o.dtype, h.d_model, h.d_model);
-        upd(L.gate.dtype, 2 * h.d_ffn, h.d_model);
-        upd(L.down.dtype, h.d_model, h.d_ffn);
+        const QkvRuns R = qkv_runs(L, h);
+        for (int r = 0; r < R.n; r++) f(R.dt[r], R.rows[r], h.d_model, layer_fold(d, R.rows[r], h.d_model));
+        f(L.o.dtype, h.d_model, h.d_model, layer_fold(d, h.d_model, h.d_model));
+        f(L.gate.dtype, 2 * h.d_ffn, h.d_model, layer_fold(d, 2 * h.d_ffn, h.d_model));
+        f(L.down.dtype, h.d_model, h.d_ffn, layer_fold(d, h.d_model, h.d_ffn));
     }
     const cmolhip_host_tensor_t &lm = d->lm_head.data ? d->lm_head : d->embd;
-    const QTensor t = shape_qt(lm.dtype, h.vocab, h.d_model, head_fold(d));
+    f(lm.dtype, h.vocab, h.d_model, head_fold(d));
+}
+
+// k-split scratch (floats) the matvecs of one step of n vectors need: the
+// largest over the step's launches (they run one after another on one
+// stream, so they share the buffer).
+size_t step_part_floats(const cmolhip_model_desc_t *d, int n)
+{
+    size_t m = 0;
+    for_each_step_matvec(d, [&](int dt, int rows, int cols, int fold) {
+        const size_t f = gemv_part_floats(shape_qt(dt, rows, cols, fold), n);
+        m = f > m ? f : m;
+    });
+    return m;
+}
+
+// Scratch for a batch of up to cap vectors: the largest step need over
+// 1..cap (the split count depends on the batch size).
+size_t batch_part_floats(const cmolhip_model_desc_t *d, int cap)
+{
+    size_t m = 0;
     for (int n = 1; n <= cap; n++) {
-        const size_t f = gemv_part_floats(t, n);
+        const size_t f = step_part_floats(d, n);
         m = f > m ? f : m;
     }
     return m;
@@ -887,14 +911,8 @@ Plan make_plan(const cmolhip_model_desc_t *d)
     P.add(P.staging);
     for (int l = 0; l < h.n_layers; l++) {
         const auto &L = d->layers[l];
-        int first[3], count[3];
-        const int nr = qkv_runs(L, first, count);
-        for (int r = 0; r < nr; r++) {
-            int rows = 0;
-            for (int p = first[r]; p < first[r] + count[r]; p++) rows += qkv_part_rows(h, p);
-            const int dt = r == 0 ? L.q.dtype : first[r] == 1 ? L.k.dtype : L.v.dtype;
-            add_q(P, dt, rows, h.d_model, layer_fold(d, rows, h.d_model));
-        }
+        const QkvRuns R = qkv_runs(L, h);
+        for (int r = 0; r < R.n; r++) add_q(P, R.dt[r], R.rows[r], h.d_model, layer_fold(d, R.rows[r], h.d_model));
         add_q(P, L.o.dtype, h.d_model, h.d_model, layer_fold(d, h.d_model, h.d_model));
         add_q(P, L.gate.dtype, 2 * h.d_ffn, h.d_model, layer_fold(d, 2 * h.d_ffn, h.d_model));
         add_q(P, L.down.dtype, h.d_model, h.d_ffn, layer_fold(d, h.d_model, h.d_ffn));
@@ -1055,6 +1073,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         g.pos = B.steps + 1;
         g.pos_stride = 3;
         g.part = B.part;
+        g.part_cap = B.part_cap;
         if (L.q_norm || L.k_norm) {
             RC(enqueue_qk_norm(m, L, g, B.qkv_raw, g.kv, n, st, false));
         } else {
@@ -1094,6 +1113,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         go.n = n;
         go.next = act_out(B.op_gu, L.gu.dtype, n, L.ffn_norm, B.ss_b, P);
         go.part = B.part;
+        go.part_cap = B.part_cap;
         RC(launch_gemv(go, EPI_RESID, st));
 
         GemvArgs gu{};
@@ -1103,6 +1123,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         gu.n = n;
         gu.next = act_out(B.op_dn, L.down.dtype, n, nullptr, nullptr, 0);
         gu.part = B.part;
+        gu.part_cap = B.part_cap;
         RC(launch_gemv(gu, EPI_SWIGLU, st));
 
         GemvArgs gd{};
@@ -1116,6 +1137,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         else
             gd.next = act_out(B.op_lm, lm_tensor(m).dtype, n, m->out_norm, B.ss_a, P);
         gd.part = B.part;
+        gd.part_cap = B.part_cap;
         RC(launch_gemv(gd, EPI_RESID, st));
         ss_count = L.down.row_tiles;
     }
@@ -1127,6 +1149,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
     gl.n = n;
     gl.argmax = B.argmax;
     gl.part = B.part;
+    gl.part_cap = B.part_cap;
     RC(launch_gemv(gl, EPI_LOGITS, st));
     return E_OK;
 }
@@ -1292,6 +1315,7 @@ int build_batch(cmolhip_model *m, Batch &B, int cap, size_t part_floats)
     RC(arena_get(c, (size_t)cap * np, &B.pl));
     RC(arena_get(c, (size_t)cap * np * h.d_head, &B.po));
     if (part_floats) RC(arena_get(c, part_floats, &B.part));
+    B.part_cap = part_floats;
     if (m->qk_norm) RC(arena_get(c, (size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head), &B.qkv_raw));
     HC(hipMemsetAsync(B.steps, 0, (size_t)cap * 12, c->stream));
     HC(hipStreamCreateWithFlags(&B.st, hipStreamNonBlocking));
@@ -1480,15 +1504,13 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
         const cmolhip_layer_tensors_t &T = d->layers[l];
         MLayer &L = m->layers[l];
         const cmolhip_host_tensor_t *qkv[3] = {&T.q, &T.k, &T.v};
-        int first[3], count[3];
-        L.n_qkv = qkv_runs(T, first, count);
-        for (int r = 0, row0 = 0; r < L.n_qkv; r++) {
-            int rows = 0;
-            for (int p = first[r]; p < first[r] + count[r]; p++) rows += qkv_part_rows(h, p);
+        const QkvRuns R = qkv_runs(T, h);
+        L.n_qkv = R.n;
+        for (int r = 0, row0 = 0; r < R.n; r++) {
             L.qkv_row0[r] = row0;
-            RC(upload_q(c, count[r], qkv + first[r], CMOLHIP_PARTS_CONCAT, layer_fold(d, rows, h.d_model),
-                        stg, P.staging, &L.qkv[r]));
-            row0 += rows;
+            RC(upload_q(c, R.count[r], qkv + R.first[r], CMOLHIP_PARTS_CONCAT,
+                        layer_fold(d, R.rows[r], h.d_model), stg, P.staging, &L.qkv[r]));
+            row0 += R.rows[r];
         }
         const cmolhip_host_tensor_t *o[1] = {&T.o};
         RC(upload_q(c, 1, o, CMOLHIP_PARTS_CONCAT, layer_fold(d, h.d_model, h.d_model), stg,
@@ -1643,6 +1665,22 @@ int cmolhip_model_plan(const cmolhip_model_desc_t *desc, size_t *device_bytes)
     return E_OK;
 }
 
+size_t cmolhip_gemv_scratch_floats(int dtype, int rows, int cols, int fold, int n)
+{
+    if (!is_block_fmt(dtype) || rows < 1 || cols < 32 || cols % 32 || n < 1 || n > 32 ||
+        (fold != 1 && fold != 2 && fold != 4 && fold != 8))
+        return 0;
+    return gemv_part_floats(shape_qt(dtype, rows, cols, fold), n);
+}
+
+int cmolhip_batch_scratch_floats(const cmolhip_model_desc_t *desc, int cap, size_t *floats)
+{
+    if (!floats || cap < 1 || cap > 32) return E_ARGS;
+    RC(validate_desc(desc));
+    *floats = batch_part_floats(desc, cap);
+    return E_OK;
+}
+
 int cmolhip_model_create(const cmolhip_model_desc_t *desc, int device, cmolhip_model_t **out)
 {
     if (!out) return E_ARGS;
@@ -1788,11 +1826,25 @@ int decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t 
     }
     Batch &B = *m->multi;
     std::lock_guard<std::mutex> g(B.mu);
-    // the KV caches of these sessions are written: exclude their own decodes
-    std::vector<std::unique_lock<std::mutex>> held;
-    std::vector<int> order(slots, slots + n);
-    std::sort(order.begin(), order.end());
-    for (int s : order) held.emplace_back(m->slots[s]->mu);
+    // the KV caches of these sessions are written: exclude their own decodes,
+    // locking the slots in ascending order (fixed arrays: a step allocates
+    // nothing)
+    int order[32];
+    for (int i = 0; i < n; i++) {
+        int j = i;
+        for (; j > 0 && order[j - 1] > slots[i]; j--) order[j] = order[j - 1];
+        order[j] = slots[i];
+    }
+    for (int i = 0; i < n; i++) m->slots[order[i]]->mu.lock();
+    struct Unlock {
+        cmolhip_model_t *m;
+        const int *order;
+        int n;
+        ~Unlock()
+        {
+            for (int i = n - 1; i >= 0; i--) m->slots[order[i]]->mu.unlock();
+        }
+    } unlock{m, order, n};
     for (int i = 0; i < n; i++) {
         B.h_steps[3 * i + 0] = tokens[i];
         B.h_steps[3 * i + 1] = pos[i];

@@ -839,7 +839,7 @@ static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
     sh.epi = epi;
     sh.ss_count = a.in.ss ? a.in.ss_count : 0;
     const int wgs = gb_plan(a.w, a.n, sh);
-    if (sh.splits > 1 && !a.part) return -6;
+    if (sh.splits > 1 && (!a.part || (size_t)sh.splits * a.n * a.w.rows > a.part_cap)) return -6;
     const long blocks = (long)((sh.rblocks * sh.splits + 7) / 8) * 8 * sh.groups;
     const size_t lds = (size_t)4 * sh.sq * 1024 + ((GB_VG * sh.ss_count + 3) & ~3) * 4 + GB_VG * 4;
     (void)wgs;

@@ -236,9 +236,10 @@ struct GemvArgs {
     unsigned long long *argmax;   // ARGMAX_SLOTS slots per vector
     // when set, recorded at the kernel's own start and end (kernel timing)
     hipEvent_t ev_start, ev_stop;
-    // batches of more than 8 vectors: k-split partial sums, at least
-    // gemv_part_floats(w, n) floats (unused when that is 0)
+    // batches of more than 8 vectors: k-split partial sums of part_cap
+    // floats; a launch needing more (gemv_part_floats(w, n)) is refused
     float *part;
+    size_t part_cap;
 };
 
 int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);
@@ -376,6 +377,10 @@ int persist_capacity_q5(int d_head, int kv_f16, int lds);
 int persist_capacity_q8(int d_head, int kv_f16, int lds);
 
 // ---- misc.hip
+// dst[cols][rows] = transpose of src[rows][cols] (fp32).
+int launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s);
+// out[i] = i, i < n.
+int launch_iota(int32_t *out, int n, hipStream_t s);
 int launch_kv_synth(void *kc, void *vc, int n_kv, int max_ctx, int d_head,
                     int n_tokens, int kv_f16, uint64_t seed, hipStream_t s);
 int launch_kv_convert(const void *src, float *dst, int n_kv, int max_ctx,

@@ -128,3 +128,43 @@ int launch_act_extract(const _Float16 *src, int K, int n, int v, _Float16 *dst, 
                        ss_src, ss_stride, ss_count, ss_dst);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
+
+// dst[c][r] = src[r][c] for a rows x cols fp32 matrix (the host seam's
+// k-major activations and [m][n] outputs against the matvec's [n][k]).
+__global__ void k_transpose(const float *__restrict__ src, float *__restrict__ dst, int rows, int cols)
+{
+    __shared__ float t[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8 threads
+    for (int i = ty; i < 32; i += 8) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) t[i][tx] = src[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int c = c0 + i, r = r0 + tx;
+        if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][i];
+    }
+}
+
+int launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s)
+{
+    if (rows < 1 || cols < 1) return 0;
+    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
+    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, s, src, dst, rows, cols);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// out[i] = i for i < n.
+__global__ void k_iota(int32_t *out, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = i;
+}
+
+int launch_iota(int32_t *out, int n, hipStream_t s)
+{
+    if (n < 1) return 0;
+    hipLaunchKernelGGL(k_iota, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, n);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}

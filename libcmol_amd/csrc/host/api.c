@@ -314,9 +314,12 @@ static cmol_model_t *load_model(const char *path, const cmol_config_t *cfg, cmol
     }
     m->pool_free = c.max_sessions == 32 ? 0xFFFFFFFFu : (1u << c.max_sessions) - 1u;
     if (pthread_mutex_init(&m->pool_lock, NULL) != 0) FAIL(CMOL_ERR_OOM);
+    cmol_sampler_pool_start();   /* the sampler's threads exist before the first draw */
+    m->sampler_held = 1;
     if (c.max_sessions > 1 && env_batch()) {
         if (cmol_sched_init(&m->sched, run_steps, m, env_batch_wait_us()) != CMOL_OK) {
             pthread_mutex_destroy(&m->pool_lock);
+            cmol_sampler_pool_stop();
             FAIL(CMOL_ERR_OOM);
         }
         m->sched_on = 1;
@@ -347,6 +350,7 @@ void cmol_free(cmol_model_t *m)
     if (!m) return;
     pthread_mutex_destroy(&m->pool_lock);
     if (m->sched_on) cmol_sched_destroy(&m->sched);
+    if (m->sampler_held) cmol_sampler_pool_stop();
     cmolhip_model_destroy(m->dev);
     cmol_mmap_close(&m->mmap);
     free(m->arena_buf);

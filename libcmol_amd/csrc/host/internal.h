@@ -128,6 +128,7 @@ struct cmol_model {
     int kv_f16;
     cmol_sched_t sched;       /* batches concurrent decode steps (max_sessions > 1) */
     int sched_on;
+    int sampler_held;            /* this model holds a start of the sampler pool */
 };
 
 struct cmol_session {
@@ -178,6 +179,10 @@ void cmol_rng_seed(uint64_t state[4], unsigned int seed);
 uint64_t cmol_rng_next(uint64_t state[4]);
 void cmol_apply_repeat_penalty(float *logits, int vocab_size, const int32_t *tokens,
                                int n_tokens, float penalty);
+/* The softmax worker pool: started by every cmol_load, stopped by every
+ * cmol_free; the first start creates the threads, the last stop joins them. */
+void cmol_sampler_pool_start(void);
+void cmol_sampler_pool_stop(void);
 
 /* api.c */
 void cmol_log(const cmol_model_t *m, int level, const char *fmt, ...);

@@ -50,16 +50,25 @@ static uint64_t splitmix(uint64_t *x)
     return z ^ (z >> 31);
 }
 
+/* Seed 0 asks for a non-reproducible stream: 8 bytes from the kernel's
+ * entropy source, or, where that is unavailable, the monotonic clock in
+ * nanoseconds with a process-wide call counter; either way splitmix64 then
+ * expands the value as it does a caller's seed. */
+static uint64_t fresh_seed(void)
+{
+    uint64_t x = 0;
+    if (getentropy(&x, sizeof x) == 0 && x) return x;
+    static uint64_t calls = 0;
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    const uint64_t c = __atomic_add_fetch(&calls, 1, __ATOMIC_RELAXED);
+    x = (uint64_t)t.tv_sec * 1000000000ull + (uint64_t)t.tv_nsec;
+    return x + (c << 40) + c;
+}
+
 void cmol_rng_seed(uint64_t st[4], unsigned int seed)
 {
-    uint64_t x;
-    if (seed == 0) {
-        static uint64_t counter = 0;
-        x = (uint64_t)time(NULL) ^ (++counter * 6364136223846793005ull) ^ (uint64_t)(uintptr_t)st;
-        if (!x) x = 0xDEADBEEFCAFEBABEull;
-    } else {
-        x = (uint64_t)seed;
-    }
+    uint64_t x = seed ? (uint64_t)seed : fresh_seed();
     for (int i = 0; i < 4; i++) st[i] = splitmix(&x);
 }
 
@@ -103,21 +112,30 @@ static void softmax_inplace(float *x, int n)
 #define POOL_MAX 16
 enum { PH_SCALE_MAX, PH_EXP, PH_SCALE };
 
+/* The pool lives while a model is loaded: cmol_load starts it (the first
+ * load creates the workers) and cmol_free stops it (the last free wakes the
+ * workers with `stop` set and joins them), so no thread is created on a
+ * decode path and none outlives the library's last model. */
 static struct {
     pthread_mutex_t mu;
     pthread_cond_t go, done;
-    pthread_once_t once;
+    int refs;                 /* loaded models (and harness holds) */
     int created;              /* worker threads */
     int used;                 /* workers a softmax uses (<= created) */
     int min_vocab;            /* smaller vocabularies run single-threaded */
     int busy;                 /* a caller owns the pool */
+    int stop;                 /* workers exit */
     unsigned gen;             /* job generation */
+    unsigned gen0;            /* generation when the workers were created */
     int left;                 /* workers still on the current job */
     int phase, V, parts;
     float *x, a;
     float cmax[POOL_MAX + 1];
-} pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_ONCE_INIT,
-          0, 0, 16384, 0, 0, 0, 0, 0, 0, NULL, 0.0f, {0}};
+    pthread_t tid[POOL_MAX];
+} pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER,
+          0, 0, 0, 16384, 0, 0, 0, 0, 0, 0, 0, 0, NULL, 0.0f, {0}, {0}};
+static pthread_mutex_t pool_life = PTHREAD_MUTEX_INITIALIZER;   /* start / stop */
+static int pool_threads_wanted = -1;   /* cmol__sampler_config before the start */
 
 /* Part j of the current job: elements [V j / parts, V (j+1) / parts). */
 static void pool_part(int j)
@@ -156,13 +174,17 @@ static uint64_t pool_now_ns(void)
 static void *pool_worker(void *arg)
 {
     const int j = (int)(intptr_t)arg;
-    unsigned seen = 0;
+    unsigned seen = pool.gen0;   /* jobs before this pool's start are not ours */
     for (;;) {
         const uint64_t t0 = pool_now_ns();
         while (__atomic_load_n(&pool.gen, __ATOMIC_ACQUIRE) == seen && pool_now_ns() - t0 < POOL_SPIN_NS)
             __builtin_ia32_pause();
         pthread_mutex_lock(&pool.mu);
-        while (pool.gen == seen) pthread_cond_wait(&pool.go, &pool.mu);
+        while (pool.gen == seen && !pool.stop) pthread_cond_wait(&pool.go, &pool.mu);
+        if (pool.stop) {
+            pthread_mutex_unlock(&pool.mu);
+            return NULL;
+        }
         seen = pool.gen;
         pthread_mutex_unlock(&pool.mu);
         pool_part(j);
@@ -170,31 +192,73 @@ static void *pool_worker(void *arg)
         if (--pool.left == 0) pthread_cond_signal(&pool.done);
         pthread_mutex_unlock(&pool.mu);
     }
-    return NULL;
 }
 
-/* Worker count: CMOL_SAMPLER_THREADS, else half the online CPUs, at most 8. */
-static void pool_init(void)
+/* Worker count: cmol__sampler_config's, else CMOL_SAMPLER_THREADS, else half
+ * the online CPUs, at most 8. */
+static int pool_size(void)
 {
+    if (pool_threads_wanted >= 0) return pool_threads_wanted;
     const char *e = getenv("CMOL_SAMPLER_THREADS");
     long n = e ? atol(e) : sysconf(_SC_NPROCESSORS_ONLN) / 2;
     if (!e && n > 8) n = 8;
     if (n < 0) n = 0;
     if (n > POOL_MAX) n = POOL_MAX;
-    int made = 0;
-    for (int j = 1; j <= n; j++) {
-        pthread_t t;
-        if (pthread_create(&t, NULL, pool_worker, (void *)(intptr_t)j) != 0) break;
-        pthread_detach(t);
-        made++;
-    }
-    pthread_mutex_lock(&pool.mu);
-    pool.created = made;
-    pool.used = made;
-    pthread_mutex_unlock(&pool.mu);
+    return (int)n;
 }
 
-/* Runs one phase on the workers and the caller (part 0); pool.mu held. */
+void cmol_sampler_pool_start(void)
+{
+    pthread_mutex_lock(&pool_life);
+    if (pool.refs++ == 0) {
+        const int n = pool_size();
+        int made = 0;
+        pthread_mutex_lock(&pool.mu);
+        pool.stop = 0;
+        pool.left = 0;
+        pool.gen0 = pool.gen;
+        pthread_mutex_unlock(&pool.mu);
+        for (int j = 1; j <= n; j++) {
+            if (pthread_create(&pool.tid[made], NULL, pool_worker, (void *)(intptr_t)j) != 0) break;
+            made++;
+        }
+        pthread_mutex_lock(&pool.mu);
+        pool.created = made;
+        pool.used = made;
+        pthread_mutex_unlock(&pool.mu);
+    }
+    pthread_mutex_unlock(&pool_life);
+}
+
+void cmol_sampler_pool_stop(void)
+{
+    pthread_mutex_lock(&pool_life);
+    if (pool.refs > 0 && --pool.refs == 0) {
+        pthread_mutex_lock(&pool.mu);
+        const int n = pool.created;
+        pool.stop = 1;
+        pool.created = 0;
+        pool.used = 0;
+        __atomic_store_n(&pool.gen, pool.gen + 1, __ATOMIC_RELEASE);
+        pthread_cond_broadcast(&pool.go);
+        pthread_mutex_unlock(&pool.mu);
+        for (int j = 0; j < n; j++) pthread_join(pool.tid[j], NULL);
+    }
+    pthread_mutex_unlock(&pool_life);
+}
+
+int cmol__sampler_pool(int on)
+{
+    if (on) cmol_sampler_pool_start();
+    else cmol_sampler_pool_stop();
+    pthread_mutex_lock(&pool.mu);
+    const int n = pool.created;
+    pthread_mutex_unlock(&pool.mu);
+    return n;
+}
+
+/* Runs one phase on the workers and the caller (part 0); pool.mu held.
+ * Every created worker takes part (parts beyond pool.parts do nothing). */
 static void pool_run(int phase, float a)
 {
     pool.phase = phase;
@@ -216,7 +280,6 @@ static void pool_run(int phase, float a)
  * or the vocabulary small. */
 static int pool_softmax(float *x, int V, float inv_t)
 {
-    pthread_once(&pool.once, pool_init);
     pthread_mutex_lock(&pool.mu);
     if (pool.busy || pool.used < 1 || V < pool.min_vocab) {
         pthread_mutex_unlock(&pool.mu);
@@ -244,12 +307,16 @@ static int pool_softmax(float *x, int V, float inv_t)
 
 int cmol__sampler_config(int threads, int min_vocab)
 {
-    pthread_once(&pool.once, pool_init);
+    pthread_mutex_lock(&pool_life);
     pthread_mutex_lock(&pool.mu);
-    const int prev = pool.used;
-    if (threads >= 0) pool.used = threads < pool.created ? threads : pool.created;
+    const int prev = pool.refs ? pool.used : pool_size();
+    if (threads >= 0) {
+        if (pool.refs) pool.used = threads < pool.created ? threads : pool.created;
+        else pool_threads_wanted = threads > POOL_MAX ? POOL_MAX : threads;
+    }
     if (min_vocab > 0) pool.min_vocab = min_vocab;
     pthread_mutex_unlock(&pool.mu);
+    pthread_mutex_unlock(&pool_life);
     return prev;
 }
 

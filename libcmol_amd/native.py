@@ -94,6 +94,8 @@ SIGNATURES = [
     ("cmolhip_attn_decode", C.c_int, [P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int,
                                       C.c_int, C.c_int, C.c_int, P]),
     ("cmolhip_model_plan", C.c_int, [P, C.POINTER(C.c_size_t)]),
+    ("cmolhip_gemv_scratch_floats", C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("cmolhip_batch_scratch_floats", C.c_int, [P, C.c_int, C.POINTER(C.c_size_t)]),
     ("cmolhip_model_create", C.c_int, [P, C.c_int, C.POINTER(P)]),
     ("cmolhip_model_destroy", None, [P]),
     ("cmolhip_model_ctx", P, [P]),
@@ -120,12 +122,70 @@ SIGNATURES = [
     ("cmol_rng_next", C.c_uint64, [P]),
     ("cmol_apply_repeat_penalty", None, [P, C.c_int, P, C.c_int, C.c_float]),
     ("cmol__sampler_config", C.c_int, [C.c_int, C.c_int]),
+    ("cmol__sampler_pool", C.c_int, [C.c_int]),
     ("cmol__sched_stats", C.c_int, [P, P]),
     ("cmol__sched_selftest", C.c_int, [C.c_int, C.c_int, C.c_long, C.c_long, C.c_uint, P]),
     ("cmol__session_length", C.c_int, [P]),
     ("cmol__session_slot", C.c_int, [P]),
     ("cmol__device", P, [P]),
 ]
+
+
+
+class HParams(C.Structure):
+    """cmolhip_hparams_t"""
+    _fields_ = [(n, C.c_int32) for n in (
+        "n_layers", "n_heads", "n_kv_heads", "d_model", "d_head", "d_ffn", "vocab",
+        "max_ctx", "max_sessions", "no_rope_interval", "kv_f16", "prefill_chunk")] + [
+        ("rope_base", C.c_float), ("rms_eps", C.c_float)]
+
+
+class HostTensor(C.Structure):
+    """cmolhip_host_tensor_t"""
+    _fields_ = [("data", P), ("dtype", I32), ("rows", I32), ("cols", I32)]
+
+
+class LayerTensors(C.Structure):
+    """cmolhip_layer_tensors_t"""
+    _fields_ = [(n, HostTensor) for n in (
+        "attn_norm", "q", "k", "v", "o", "q_norm", "k_norm", "ffn_norm", "gate", "up", "down")]
+
+
+class ModelDesc(C.Structure):
+    """cmolhip_model_desc_t"""
+    _fields_ = [("hp", HParams), ("embd", HostTensor), ("out_norm", HostTensor),
+                ("lm_head", HostTensor), ("layers", C.POINTER(LayerTensors)),
+                ("rope_table", P)]
+
+
+def shape_desc(hp: HParams, q, k, v, o, gate, down, embd, lm=None):
+    """A model description with shapes and formats only, for the device-free
+    planning calls (the data pointers point at a dummy byte: planning never
+    reads weights).  Returns (desc, keepalive)."""
+    dummy = (C.c_uint8 * 16)()
+    addr = C.cast(dummy, P)
+    d, kvd = hp.d_model, hp.n_kv_heads * hp.d_head
+
+    def t(dt, rows, cols):
+        return HostTensor(addr, dt, rows, cols)
+
+    layers = (LayerTensors * hp.n_layers)()
+    for L in layers:
+        L.attn_norm = t(0, 1, d)
+        L.ffn_norm = t(0, 1, d)
+        L.q, L.k, L.v = t(q, d, d), t(k, kvd, d), t(v, kvd, d)
+        L.o = t(o, d, d)
+        L.gate, L.up = t(gate, hp.d_ffn, d), t(gate, hp.d_ffn, d)
+        L.down = t(down, d, hp.d_ffn)
+    desc = ModelDesc()
+    desc.hp = hp
+    desc.embd = t(embd, hp.vocab, d)
+    desc.out_norm = t(0, 1, d)
+    desc.lm_head = t(lm, hp.vocab, d) if lm is not None else HostTensor(None, 0, 0, 0)
+    desc.layers = layers
+    desc.rope_table = addr
+    return desc, (dummy, layers)
+
 
 _lib = None
 

@@ -115,11 +115,13 @@ def test_sampler_pool_matches_reference(ci):
     """The same reference draws with the softmax's element-wise parts on the
     worker pool (forced on for this small vocabulary)."""
     L = native.lib()
+    assert L.cmol__sampler_pool(1) >= 1   # a hold, as cmol_load takes
     prev = L.cmol__sampler_config(4, 1)
     try:
         test_sampler_matches_reference(ci)
     finally:
         L.cmol__sampler_config(prev, 16384)
+        L.cmol__sampler_pool(0)
 
 
 @pytest.mark.parametrize("nan", [False, True])
@@ -139,6 +141,7 @@ def test_sampler_pool_bit_identical(params, nan):
         base[12345] = np.nan
     prm = native.default_params(**params)
     out = {}
+    assert L.cmol__sampler_pool(1) >= 1
     for threads in (0, 4):
         prev = L.cmol__sampler_config(threads, 16384)
         st = np.zeros(4, np.uint64)
@@ -150,6 +153,7 @@ def test_sampler_pool_bit_identical(params, nan):
             probs = lg
         L.cmol__sampler_config(prev, 16384)
         out[threads] = (ids, probs.view(np.uint32))
+    L.cmol__sampler_pool(0)
     assert out[0][0] == out[4][0]
     assert np.array_equal(out[0][1], out[4][1])
     if not nan:
@@ -232,3 +236,44 @@ def test_sampler_top_k_matches_reference_full_vocab(k, p):
         ib = R.cmol_sample(C.c_void_p(b.ctypes.data), C.c_int(V), C.byref(prm), C.c_void_p(st_b.ctypes.data))
         assert ia == ib, f"draw {d}"
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"draw {d}"
+
+
+def test_sampler_pool_lifetime():
+    """The worker pool exists only while held (cmol_load holds it until
+    cmol_free): holds nest, the last release joins every worker, and a draw
+    without the pool runs single-threaded with the same result."""
+    L, V = native.lib(), 40000
+    while L.cmol__sampler_pool(0) > 0:   # drop holds left by other tests
+        pass
+    rng = np.random.default_rng(3)
+    base = rng.standard_normal(V).astype(np.float32)
+    prm = native.default_params(temperature=1.0, top_k=0, top_p=1.0)
+
+    def draw():
+        st = np.zeros(4, np.uint64)
+        L.cmol_rng_seed(st.ctypes.data, 5)
+        lg = base.copy()
+        return int(L.cmol_sample(lg.ctypes.data, V, prm, st.ctypes.data)), lg.view(np.uint32).copy()
+
+    alone = draw()
+    prev = L.cmol__sampler_config(3, 16384)   # size of the next pool
+    n1 = L.cmol__sampler_pool(1)
+    n2 = L.cmol__sampler_pool(1)
+    assert n1 == n2 == 3
+    pooled = draw()
+    assert L.cmol__sampler_pool(0) == 3   # one hold left
+    assert L.cmol__sampler_pool(0) == 0   # joined
+    L.cmol__sampler_config(prev, 16384)
+    assert pooled[0] == alone[0] and np.array_equal(pooled[1], alone[1])
+    assert draw()[0] == alone[0]
+
+
+def test_seed_zero_streams_differ():
+    """Seed 0 asks for a fresh, non-reproducible stream on every call."""
+    L = native.lib()
+    firsts = set()
+    for _ in range(8):
+        st = np.zeros(4, np.uint64)
+        L.cmol_rng_seed(st.ctypes.data, 0)
+        firsts.add(int(L.cmol_rng_next(st.ctypes.data)))
+    assert len(firsts) == 8
