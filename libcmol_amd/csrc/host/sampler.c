@@ -180,16 +180,19 @@ static void *pool_worker(void *arg)
         while (__atomic_load_n(&pool.gen, __ATOMIC_ACQUIRE) == seen && pool_now_ns() - t0 < POOL_SPIN_NS)
             __builtin_ia32_pause();
         pthread_mutex_lock(&pool.mu);
-        while (pool.gen == seen && !pool.stop) pthread_cond_wait(&pool.go, &pool.mu);
+        while (__atomic_load_n(&pool.gen, __ATOMIC_RELAXED) == seen && !pool.stop)
+            pthread_cond_wait(&pool.go, &pool.mu);
         if (pool.stop) {
             pthread_mutex_unlock(&pool.mu);
             return NULL;
         }
-        seen = pool.gen;
+        seen = __atomic_load_n(&pool.gen, __ATOMIC_RELAXED);
         pthread_mutex_unlock(&pool.mu);
         pool_part(j);
+        /* the release publishes this part's results to a caller that sees
+         * left reach 0 with its acquire load, spinning or after the wait */
         pthread_mutex_lock(&pool.mu);
-        if (--pool.left == 0) pthread_cond_signal(&pool.done);
+        if (__atomic_sub_fetch(&pool.left, 1, __ATOMIC_ACQ_REL) == 0) pthread_cond_signal(&pool.done);
         pthread_mutex_unlock(&pool.mu);
     }
 }
@@ -215,8 +218,8 @@ void cmol_sampler_pool_start(void)
         int made = 0;
         pthread_mutex_lock(&pool.mu);
         pool.stop = 0;
-        pool.left = 0;
-        pool.gen0 = pool.gen;
+        __atomic_store_n(&pool.left, 0, __ATOMIC_RELAXED);
+        pool.gen0 = __atomic_load_n(&pool.gen, __ATOMIC_RELAXED);
         pthread_mutex_unlock(&pool.mu);
         for (int j = 1; j <= n; j++) {
             if (pthread_create(&pool.tid[made], NULL, pool_worker, (void *)(intptr_t)j) != 0) break;
@@ -263,7 +266,7 @@ static void pool_run(int phase, float a)
 {
     pool.phase = phase;
     pool.a = a;
-    pool.left = pool.created;
+    __atomic_store_n(&pool.left, pool.created, __ATOMIC_RELAXED);
     __atomic_store_n(&pool.gen, pool.gen + 1, __ATOMIC_RELEASE);
     pthread_cond_broadcast(&pool.go);
     pthread_mutex_unlock(&pool.mu);
@@ -272,7 +275,7 @@ static void pool_run(int phase, float a)
     while (__atomic_load_n(&pool.left, __ATOMIC_ACQUIRE) > 0 && pool_now_ns() - t0 < POOL_SPIN_NS)
         __builtin_ia32_pause();
     pthread_mutex_lock(&pool.mu);
-    while (pool.left > 0) pthread_cond_wait(&pool.done, &pool.mu);
+    while (__atomic_load_n(&pool.left, __ATOMIC_ACQUIRE) > 0) pthread_cond_wait(&pool.done, &pool.mu);
 }
 
 /* Temperature scale and softmax of x[0..V) on the pool, with the results of

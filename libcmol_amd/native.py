@@ -42,7 +42,7 @@ def default_params(**kw) -> GenParams:
 
 
 def greedy_params(max_new: int, **kw) -> GenParams:
-    return default_params(temperature=0.0, repeat_penalty=1.0, max_new_tokens=max_new, **kw)
+    return default_params(**{"temperature": 0.0, "repeat_penalty": 1.0, "max_new_tokens": max_new, **kw})
 
 
 class QTensor(C.Structure):
@@ -459,3 +459,26 @@ def decode_batch(sessions, tokens) -> np.ndarray:
     out = np.zeros(n, np.int32)
     check(lib().cmol__decode_batch(arr, ptr(t), n, ptr(out)), "decode_batch")
     return out
+
+
+def decode_batch_logits(model: Model, sessions, tokens, pos, vocab: int):
+    """One lock-step step of `sessions` at their own positions through
+    cmolhip_decode_batch: (next ids, logits [n][vocab]).  Session lengths are
+    the caller's to track."""
+    n = len(sessions)
+    slots = np.array([s.slot for s in sessions], np.int32)
+    t = np.ascontiguousarray(tokens, np.int32)
+    p = np.ascontiguousarray(pos, np.int32)
+    lg = np.zeros((n, vocab), np.float32)
+    out = np.zeros(n, np.int32)
+    check(lib().cmolhip_decode_batch(model.device, n, ptr(slots), ptr(t), ptr(p), ptr(lg), ptr(out)),
+          "decode_batch")
+    return out, lg
+
+
+def kv_download(model: Model, slot: int, layer: int, n: int, kvd: int):
+    """K and V rows [n][kvd] of one layer of a session's cache, as fp32."""
+    k = np.zeros((n, kvd), np.float32)
+    v = np.zeros((n, kvd), np.float32)
+    check(lib().cmolhip_kv_download(model.device, slot, layer, n, ptr(k), ptr(v)), "kv_download")
+    return k, v

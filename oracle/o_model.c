@@ -362,6 +362,7 @@ static void mm(o_model_t *m, float *out, const o_tensor_t *t, const float *x, in
 struct o_sess {
     o_model_t *m;
     int max_ctx;
+    int kv_f16;              /* round K/V to fp16 on write */
     float *k, *v;            /* [L][max_ctx][n_kv][d_head] */
     float *x, *xn, *q, *kb, *vb, *sc, *ao, *g, *u, *logits;
 };
@@ -397,6 +398,8 @@ void o_sess_free(o_sess_t *s)
     free(s);
 }
 
+void o_sess_kv_f16(o_sess_t *s, int on) { s->kv_f16 = on != 0; }
+
 float *o_sess_k(o_sess_t *s) { return s->k; }
 float *o_sess_v(o_sess_t *s) { return s->v; }
 const float *o_sess_logits(o_sess_t *s) { return s->logits; }
@@ -429,6 +432,11 @@ const float *o_forward(o_model_t *m, o_sess_t *s, int32_t token, int pos)
         float *vc = s->v + (size_t)l * s->max_ctx * kvd;
         memcpy(kc + (size_t)pos * kvd, s->kb, (size_t)kvd * 4);
         memcpy(vc + (size_t)pos * kvd, s->vb, (size_t)kvd * 4);
+        if (s->kv_f16)
+            for (int i = 0; i < kvd; i++) {
+                kc[(size_t)pos * kvd + i] = o_f16_to_f32(o_f32_to_f16(s->kb[i]));
+                vc[(size_t)pos * kvd + i] = o_f16_to_f32(o_f32_to_f16(s->vb[i]));
+            }
         o_attention(s->q, kc, vc, pos + 1, nh, nkv, dh, s->sc, s->ao);
         memcpy(s->q, s->ao, (size_t)d * 4);
         mm(m, s->ao, t[L_O], s->q, d, d);

@@ -38,6 +38,36 @@ float o_f16_to_f32(uint16_t h)
     return r;
 }
 
+/* IEEE binary32 -> binary16, round to nearest, ties to even; overflow to
+ * +-Inf, NaN stays a quiet NaN keeping the top payload bits.  No reference
+ * counterpart (the reference caches K/V in fp32): it models the fp16 KV
+ * cache of the multi-session configuration, where each K/V value is rounded
+ * once when it is written. */
+uint16_t o_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);   /* >= 65520 (and Inf) */
+    uint32_t h, rem, half;
+    if (ax >= 0x38800000u) {                 /* normal: exponent rebias, 13 bits dropped */
+        const uint32_t r = ax - 0x38000000u;
+        h = r >> 13;
+        rem = r & 0x1FFFu;
+        half = 0x1000u;
+    } else {                                 /* subnormal half: units of 2^-24 */
+        const uint32_t e = ax >> 23;
+        if (e < 102u) return (uint16_t)sign;  /* below 2^-25 */
+        const uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u, sh = 126u - e;   /* 14..24 */
+        h = mant >> sh;
+        rem = mant & ((1u << sh) - 1u);
+        half = 1u << (sh - 1u);
+    }
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
 /* Block geometry per dtype: values per block, bytes per block.
  * Reference src/quant.c:298-308 (+ Q4_0, absent there: 18-byte blocks);
  * the K-quant super-blocks hold 256 values (src/quant.c:91-105). */

@@ -42,6 +42,7 @@ enum { O_ORDER_SCALAR = 0,   /* cmol_matmul_scalar  src/quant.c:334-376 */
        O_ORDER_AVX512 = 1 }; /* cmol_matmul_avx512  src/quant.c:488-566 */
 
 float  o_f16_to_f32(uint16_t h);
+uint16_t o_f32_to_f16(float f);
 size_t o_row_bytes(int k, int dtype);
 int    o_block_params(int dtype, size_t *bsz);
 void   o_dequant_row(const void *src, float *dst, int n, int dtype);
@@ -74,6 +75,10 @@ void       o_model_free(o_model_t *m);
 void       o_model_hparams(const o_model_t *m, int32_t out[11],
                            float out_f[2]);
 o_sess_t  *o_sess_new(o_model_t *m, int max_ctx);
+/* on != 0: every K/V value is rounded to fp16 (o_f32_to_f16) as it is
+ * written to the cache, as in an fp16 KV cache; the cache stays fp32
+ * storage.  No reference counterpart (its cache is fp32). */
+void       o_sess_kv_f16(o_sess_t *s, int on);
 void       o_sess_free(o_sess_t *s);
 /* One forward step (reference src/model.c:176-276); returns logits. */
 const float *o_forward(o_model_t *m, o_sess_t *s, int32_t token, int pos);

@@ -33,6 +33,9 @@ def lib():
         L.o_swiglu.argtypes = [P, P, P, C.c_int]
         L.o_rope_apply.argtypes = [P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
         L.o_argmax.argtypes = [P, C.c_int]; L.o_argmax.restype = C.c_int
+        L.o_f32_to_f16.argtypes = [C.c_float]; L.o_f32_to_f16.restype = C.c_uint16
+        L.o_apply_repeat_penalty.argtypes = [P, C.c_int, P, C.c_int, C.c_float]
+        L.o_sess_kv_f16.argtypes = [P, C.c_int]
         L.o_attention.argtypes = [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P]
         L.o_model_load.argtypes = [C.c_char_p, C.c_int, C.c_int]; L.o_model_load.restype = P
         L.o_model_free.argtypes = [P]
@@ -68,6 +71,18 @@ def matmul(a_bytes: np.ndarray, b: np.ndarray, m: int, k: int, dtype: int, order
     a_bytes = np.ascontiguousarray(a_bytes)
     lib().o_matmul(out.ctypes.data, a_bytes.ctypes.data, b.ctypes.data, m, k, n, dtype, order)
     return out
+
+
+def apply_repeat_penalty(logits, window, penalty):
+    out = _f32(logits).copy()
+    w = np.ascontiguousarray(window, np.int32)
+    lib().o_apply_repeat_penalty(out.ctypes.data, out.size, w.ctypes.data, w.size, penalty)
+    return out
+
+
+def f32_to_f16_bits(x):
+    x = _f32(x).ravel()
+    return np.array([lib().o_f32_to_f16(float(v)) for v in x], np.uint16)
 
 
 def rms_norm(x, w, eps):
@@ -108,7 +123,7 @@ def attention(q, kc, vc, seqlen, n_heads, n_kv, d_head):
 class Model:
     """Oracle model + one session (fp32 KV [layer][pos][n_kv][d_head])."""
 
-    def __init__(self, path: str, max_ctx: int, order: int = AVX512, nthreads: int = 0):
+    def __init__(self, path: str, max_ctx: int, order: int = AVX512, nthreads: int = 0, kv_f16: bool = False):
         nthreads = nthreads or min(16, os.cpu_count() or 1)
         self.h = lib().o_model_load(path.encode(), order, nthreads)
         if not self.h:
@@ -122,6 +137,7 @@ class Model:
         self.s = lib().o_sess_new(self.h, max_ctx)
         if not self.s:
             raise MemoryError("oracle session")
+        lib().o_sess_kv_f16(self.s, int(kv_f16))
 
     def close(self):
         if self.s:

@@ -311,3 +311,81 @@ def test_kquant_rmsnorm_prologue(ctx, dtype, n):
     xn = np.stack([O.rms_norm(xi, w, 1e-6) for xi in x])
     want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, dtype, O.AVX512).T
     assert_close(got, want, f"q{dtype} rmsnorm n {n}")
+
+
+# ---- sizes of the measured configurations --------------------------------
+@pytest.fixture
+def big_ctx(gpu):
+    c = gpu.Ctx(3 << 30)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(11008, 2048), (2048, 11008)])
+def test_ffn_shapes_full_size(gpu, big_ctx, rows, cols):
+    """The isolated matvec configuration at its size: SmolLM3-3B FFN matrices
+    of weights ~N(0, 0.02) quantised to Q4_0, activations ~N(0, 1).  The
+    whole tensor dequantises bit-exactly in the single-session fold and in
+    fold 1; the matvec at batch 1 and 8 matches the oracle."""
+    from libcmol_amd import synth
+    w = synth.normal(rows * cols, 4242 + rows, 0, 0.02)
+    raw = synth.quantize(2, w).reshape(rows, cols // 32 * 18)
+    want_deq = np.stack([O.dequant_row(raw[r], cols, 2) for r in range(rows)])
+    folds = sorted({1, gpu.lib().cmolhip_pick_fold(rows, cols, 1)})
+    x = np.random.default_rng(7).standard_normal((8, cols)).astype(np.float32)
+    want = O.matmul(raw, np.ascontiguousarray(x.T), rows, cols, 2, O.AVX512).T
+    for fold in folds:
+        t = big_ctx.qtensor([raw], 2, cols, [rows], fold=fold)
+        got = big_ctx.dequant(t)
+        assert np.array_equal(got.view(np.uint32), want_deq.view(np.uint32)), f"fold {fold}"
+        assert_close(big_ctx.gemm(t, x[:1]), want[:1], f"{rows}x{cols} fold {fold} n 1")
+        if fold == 1:
+            assert_close(big_ctx.gemm(t, x), want, f"{rows}x{cols} fold {fold} n 8")
+
+
+@pytest.mark.parametrize("rows,cols,fold", [(11008, 2048, 1), (2048, 11008, 1), (2048, 11008, 2),
+                                            (3072, 2048, 1)])
+def test_gemm_tiled_prompt_size_matches_oracle(gpu, big_ctx, rows, cols, fold):
+    """The prompt GEMM at a 2048-token prompt on the SmolLM3-3B projection
+    shapes.  Each token's output depends only on its own activation vector,
+    so 64 of the 2048 tokens (the first, the last and 62 drawn) are compared
+    with the oracle."""
+    n = 2048
+    raw = random_blocks(2, rows, cols, seed=rows + 3 * cols + fold)
+    rng = np.random.default_rng(rows)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    t = big_ctx.qtensor([raw], 2, cols, [rows], fold=fold)
+    got = big_ctx.gemm(t, x)
+    pick = np.unique(np.concatenate([[0, n - 1], rng.choice(n, 62, replace=False)]))
+    want = O.matmul(raw, np.ascontiguousarray(x[pick].T), rows, cols, 2, O.AVX512).T
+    assert_close(got[pick], want, f"tiled gemm {rows}x{cols} fold {fold} n {n}")
+
+
+# ---- the reference's kernel seam (src/cmol_internal.h:175-182) -----------
+@pytest.mark.parametrize("dtype,m,k", [(2, 96, 256), (6, 64, 512), (8, 130, 288), (12, 48, 512),
+                                       (14, 40, 768)])
+@pytest.mark.parametrize("n", [1, 3, 40])
+def test_matmul_host_seam_matches_oracle(gpu, ctx, dtype, m, k, n):
+    """cmolhip_matmul_host takes what cmol_matmul_fn_t takes: host pointers,
+    raw GGUF rows A[m][k], B k-major [k][n], out [m][n]; its result matches
+    the oracle's cmol_matmul order within 1e-4 + 1e-3*|ref|."""
+    L = gpu.lib()
+    raw = np.ascontiguousarray(random_blocks(dtype, m, k, seed=m * 11 + k + dtype))
+    b = np.random.default_rng(n + k).standard_normal((k, n)).astype(np.float32)
+    out = np.zeros((m, n), np.float32)
+    gpu.check(L.cmolhip_matmul_host(ctx.h, gpu.ptr(out), gpu.ptr(raw), gpu.ptr(b), m, k, n, dtype),
+              "matmul_host")
+    want = O.matmul(raw, b, m, k, dtype, O.AVX512)
+    assert_close(out, want, f"seam q{dtype} {m}x{k} n {n}")
+
+
+def test_matmul_host_seam_rejects_bad_arguments(gpu, ctx):
+    L = gpu.lib()
+    raw = np.zeros((4, 18), np.uint8)
+    b = np.zeros((32, 1), np.float32)
+    out = np.zeros((4, 1), np.float32)
+    args = (gpu.ptr(out), gpu.ptr(raw), gpu.ptr(b))
+    assert L.cmolhip_matmul_host(ctx.h, *args, 4, 31, 1, 2) == gpu.CMOL_ERR_ARGS
+    assert L.cmolhip_matmul_host(ctx.h, *args, 4, 32, 0, 2) == gpu.CMOL_ERR_ARGS
+    assert L.cmolhip_matmul_host(ctx.h, None, raw.ctypes.data, b.ctypes.data, 4, 32, 1, 2) == gpu.CMOL_ERR_ARGS
+    assert L.cmolhip_matmul_host(ctx.h, *args, 4, 32, 1, 0) == gpu.CMOL_ERR_UNSUPPORTED

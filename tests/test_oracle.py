@@ -365,3 +365,81 @@ def test_smollm2_135m_matches_reference(model_dir):
     toks = om.generate(G["smollm2_135m_prompt"], 128)
     assert toks.tolist() == G["smollm2_135m_tokens"].tolist()
     om.close()
+
+
+# ---- repetition penalty (reference src/sampler.c:171-184, src/api.c:465-507) --
+PEN = np.load(os.path.join(HERE, "golden", "penalty.npz"))
+
+
+@pytest.mark.parametrize("ci", range(6))
+def test_repeat_penalty_matches_reference(ci):
+    """o_apply_repeat_penalty is bit-identical to the reference's on logits
+    with +0 / -0 / negatives and windows that repeat ids or hold ids out of
+    range, for penalties at and below 1 (no-ops) and above."""
+    lg, win = PEN[f"case{ci}_logits"], PEN[f"case{ci}_window"]
+    for pi, pen in enumerate(PEN["penalties"]):
+        got = O.apply_repeat_penalty(lg, win, float(pen))
+        assert np.array_equal(bits(got), bits(PEN[f"case{ci}_p{pi}"])), (ci, float(pen))
+
+
+def test_repeat_penalty_closed_form():
+    """Each occurrence of an in-range id divides a positive logit by the
+    penalty and multiplies a non-positive one by it."""
+    lg = np.array([2.0, -3.0, 0.0, 5.0], np.float32)
+    got = O.apply_repeat_penalty(lg, [0, 1, 2, 0, 9, -1], 2.0)
+    assert got.tolist() == [0.5, -6.0, 0.0, 5.0]
+
+
+@pytest.mark.parametrize("name", ["micro-q8_0", "small-q5_0", "small-q4_0"])
+def test_greedy_with_penalty_matches_reference(name, model_dir):
+    """The oracle's generate loop with the penalty ring gives the reference's
+    greedy ids (penalty 1.3 over 64 tokens, 1.15 over 8), and the penalty
+    changes the ids (the fixture would catch a loop that ignored it)."""
+    spec = synth.PRESETS[name].replace(wstd=float(PEN[f"{name}_wstd"]))
+    path = synth.model_file(spec, model_dir)
+    prompt = PEN[f"{name}_prompt"]
+    plain = O.Model(path, 128).generate(prompt, 48)
+    for ri, (pen, last_n) in enumerate(PEN["runs"]):
+        got = O.Model(path, 128).generate(prompt, 48, penalty=float(pen), last_n=int(last_n))
+        want = PEN[f"{name}_run{ri}_ids"]
+        assert got.tolist() == want.tolist(), (name, ri)
+        assert got.tolist() != plain.tolist()
+
+
+# ---- fp16 KV cache rounding (the multi-session configuration's cache) --------
+def test_f32_to_f16_matches_numpy():
+    """Round-to-nearest-even float->half, against numpy's independent
+    conversion: every half's neighbourhood (exact values, the midpoints to
+    the next half, one ulp either side), overflow and random floats."""
+    h = np.arange(0x7C00, dtype=np.uint32)
+    lo = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    hi = (h + 1).astype(np.uint16).view(np.float16).astype(np.float32)
+    mid = ((lo.astype(np.float64) + hi.astype(np.float64)) / 2).astype(np.float32)
+    xs = np.concatenate([lo, mid, np.nextafter(mid, np.float32(0)), np.nextafter(mid, np.float32(1e9)),
+                         np.float32([65504, 65519.99, 65520, 70000, 1e30, np.inf, 0.0, 2.0**-25,
+                                     2.0**-25 * 1.0001, 2.0**-26]),
+                         np.random.default_rng(5).standard_normal(20000).astype(np.float32) * 100])
+    xs = np.concatenate([xs, -xs])
+    got = O.f32_to_f16_bits(xs)
+    want = xs.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    nan = O.f32_to_f16_bits(np.float32([np.nan]))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def test_kv_f16_session_rounds_each_write(model_dir):
+    """With the fp16 cache, layer 0's K/V at the first position are the fp32
+    session's rounded once to half (later layers see the rounded values of
+    the layers before them, so only their representability is fixed)."""
+    spec = synth.PRESETS["small-q4_0"]
+    path = synth.model_file(spec, model_dir)
+    a, b = O.Model(path, 8), O.Model(path, 8, kv_f16=True)
+    a.forward(17, 0)
+    b.forward(17, 0)
+    ka, va = a.kv()
+    kb, vb = b.kv()
+    assert np.array_equal(bits(kb[0, 0]), bits(ka[0, 0].astype(np.float16).astype(np.float32)))
+    assert np.array_equal(bits(vb[0, 0]), bits(va[0, 0].astype(np.float16).astype(np.float32)))
+    assert not np.array_equal(bits(kb[0, 0]), bits(ka[0, 0]))
+    for c in (kb, vb):
+        assert np.array_equal(bits(c[:, 0]), bits(c[:, 0].astype(np.float16).astype(np.float32)))
