@@ -109,6 +109,24 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
                                 int n, const float *ss, float eps, float *dy, void *ev_start,
                                 void *ev_stop);
 
+/* No reference counterpart.  cmolhip_gemm for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * device allocation): the same product, computed by the same kernels, with
+ * every piece of scratch (the activation operand, the RMSNorm partial sums
+ * and the batched matvec's k-split partial sums) in one fixed device array
+ * of cmolhip_noalloc_scratch_bytes() bytes (16 MiB) per GPU, held from the
+ * first cmolhip_ctx_create on that GPU until the process ends.  It calls no
+ * allocator, host or device, and does not touch the context's arena.  A call
+ * whose scratch would exceed the array (operand act_bytes(cols, n), plus
+ * n*cols/32 floats with norm_w, plus the k-split sums of 9..32 vectors)
+ * returns CMOL_ERR_ARGS without launching anything.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (other threads or
+ * other streams) race, so callers serialise them; each call writes all the
+ * scratch it reads, so nothing carries over from the previous call. */
+int cmolhip_gemm_noalloc(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx,
+                         float *dy, int n, const float *norm_w, float eps);
+size_t cmolhip_noalloc_scratch_bytes(void);
+
 /* Reference kernel seam replacement (cmol_matmul_fn_t semantics on host
  * memory): out[m][n] = A[m][k] . B[k][n], A raw GGUF rows.  Uses the
  * context arena for the transient copies; fails with CMOL_ERR_OOM when the

@@ -112,6 +112,33 @@ struct cmolhip_ctx {
     std::mutex mu;
 };
 
+// Scratch of the allocation-free entry point (cmolhip_gemm_noalloc): one
+// array per device, in the code object, held until the process ends.  Host
+// code never passes `scratch` itself (on the host the name is only a
+// stand-in): each device's address is looked up once, with that device
+// current, by resolve_scratch and kept in scratch_addr.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+static uint8_t *scratch_addr[SCRATCH_MAX_DEVICES];
+static std::mutex scratch_mu;
+
+// Device address of `scratch` on `device` (current); nullptr on failure.
+static uint8_t *resolve_scratch(int device)
+{
+    if (device < 0 || device >= SCRATCH_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> g(scratch_mu);
+    if (!scratch_addr[device]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        scratch_addr[device] = (uint8_t *)ptr;
+    }
+    return scratch_addr[device];
+}
+
 static size_t arena_mark(cmolhip_ctx_t *c)
 {
     std::lock_guard<std::mutex> g(c->mu);
@@ -147,6 +174,10 @@ int cmolhip_ctx_create(int device, size_t bytes, cmolhip_ctx_t **out)
     cmolhip_ctx_t *c = new (std::nothrow) cmolhip_ctx_t();
     if (!c) return E_OOM;
     c->device = device;
+    if (!resolve_scratch(device)) {   // once per device, this device current
+        delete c;
+        return E_UNSUPPORTED;
+    }
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return E_UNSUPPORTED;
@@ -308,12 +339,15 @@ int cmolhip_gemm_prepared(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const vo
     return cmolhip_gemm_prepared_timed(c, w, op, n, ss, eps, dy, nullptr, nullptr);
 }
 
-int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op,
-                                int n, const float *ss, float eps, float *dy, void *ev_start,
-                                void *ev_stop)
+} // extern "C"
+
+// dy[n][rows] = W . op for a prepared operand: up to 32 vectors stream the
+// weights once through the matvec (k-split partial sums in part, part_cap
+// floats), more run the tiled MFMA GEMM.
+static int launch_product(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op, int n,
+                          const float *ss, float eps, float *dy, float *part, size_t part_cap,
+                          void *ev_start, void *ev_stop)
 {
-    if (!c || !w || !op || !dy || n < 1 || n > GEMM_MAX_N || (!ev_start != !ev_stop)) return E_ARGS;
-    const size_t mark = arena_mark(c);
     GemvArgs a{};
     a.w = to_qt(*w);
     a.in.q = (const _Float16 *)op;
@@ -327,14 +361,25 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
     a.n = n;
     a.ev_start = (hipEvent_t)ev_start;
     a.ev_stop = (hipEvent_t)ev_stop;
-    // up to 32 vectors stream the weights once through the matvec; more go
-    // to the tiled MFMA GEMM.  The arena space of k-split partial sums is
-    // released at once: later work on this stream runs after the kernels.
-    int rc = E_OK;
-    const size_t pf = n <= 32 ? gemv_part_floats(a.w, n) : 0;
-    if (pf) rc = arena_get(c, pf, &a.part);
-    a.part_cap = pf;
-    if (rc == E_OK) rc = n <= 32 ? launch_gemv(a, EPI_STORE, c->stream) : launch_gemm(a, EPI_STORE, c->stream);
+    a.part = part;
+    a.part_cap = part_cap;
+    return n <= 32 ? launch_gemv(a, EPI_STORE, c->stream) : launch_gemm(a, EPI_STORE, c->stream);
+}
+
+extern "C" {
+
+int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const void *op,
+                                int n, const float *ss, float eps, float *dy, void *ev_start,
+                                void *ev_stop)
+{
+    if (!c || !w || !op || !dy || n < 1 || n > GEMM_MAX_N || (!ev_start != !ev_stop)) return E_ARGS;
+    // the arena space of k-split partial sums is released at once: later
+    // work on this stream runs after the kernels
+    const size_t mark = arena_mark(c);
+    const size_t pf = n <= 32 ? gemv_part_floats(to_qt(*w), n) : 0;
+    float *part = nullptr;
+    int rc = pf ? arena_get(c, pf, &part) : E_OK;
+    if (rc == E_OK) rc = launch_product(c, w, op, n, ss, eps, dy, part, pf, ev_start, ev_stop);
     arena_release(c, mark);
     return rc;
 }
@@ -355,6 +400,25 @@ int cmolhip_gemm(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx, 
     } while (0);
     arena_release(c, mark);
     return rc;
+}
+
+size_t cmolhip_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+int cmolhip_gemm_noalloc(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const float *dx, float *dy, int n,
+                         const float *norm_w, float eps)
+{
+    if (!c || !w || !dx || !dy || n < 1 || n > GEMM_MAX_N || w->cols < 32 || w->cols % 32) return E_ARGS;
+    uint8_t *base = scratch_addr[c->device];   // resolved when c was created
+    if (!base) return E_UNSUPPORTED;
+    // scratch layout: operand | sum-of-squares partials | k-split partial sums
+    const size_t op_b = align_up(act_bytes(w->cols, n), ALIGN);
+    const size_t ss_b = norm_w ? align_up((size_t)n * (w->cols / 32) * 4, ALIGN) : 0;
+    const size_t pf = n <= 32 ? gemv_part_floats(to_qt(*w), n) : 0;
+    if (op_b + ss_b + pf * 4 > NOALLOC_SCRATCH_BYTES) return E_ARGS;   // beyond the fixed scratch
+    float *ss = norm_w ? (float *)(base + op_b) : nullptr;
+    float *part = pf ? (float *)(base + op_b + ss_b) : nullptr;
+    RC(cmolhip_act_prepare(c, dx, n, w->cols, w->dtype, norm_w, base, ss));
+    return launch_product(c, w, base, n, ss, eps, dy, part, pf, nullptr, nullptr);
 }
 
 int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float *b, int m, int k,

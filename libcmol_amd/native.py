@@ -91,6 +91,8 @@ SIGNATURES = [
     ("cmolhip_gemm_prepared_timed", C.c_int, [P, C.POINTER(QTensor), P, C.c_int, P, C.c_float, P,
                                               P, P]),
     ("cmolhip_matmul_host", C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("cmolhip_gemm_noalloc", C.c_int, [P, C.POINTER(QTensor), P, P, C.c_int, P, C.c_float]),
+    ("cmolhip_noalloc_scratch_bytes", C.c_size_t, []),
     ("cmolhip_attn_decode", C.c_int, [P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int,
                                       C.c_int, C.c_int, C.c_int, P]),
     ("cmolhip_model_plan", C.c_int, [P, C.POINTER(C.c_size_t)]),
