@@ -201,22 +201,23 @@ cmolhip_ctx_t *cmolhip_model_ctx(cmolhip_model_t *m);
 int cmolhip_decode(cmolhip_model_t *m, int slot, int32_t token, int32_t pos,
                    float *logits_host, int32_t *argmax);
 /* 1 when cmolhip_decode runs the model's single session with the persistent
- * kernel (one cooperative launch per token, device-wide barriers between the
- * stages; opt-in with CMOL_PERSIST=1 at model creation), 0 when it replays
- * the per-kernel decode graph. */
+ * kernel (one cooperative launch per token; no device-wide barrier: each
+ * stage's readers poll the vectors they consume; opt-in with CMOL_PERSIST=1
+ * at model creation), 0 when it replays the per-kernel decode graph. */
 int cmolhip_model_persistent(cmolhip_model_t *m);
 /* Profiling of the persistent kernel (model created with CMOL_PERSIST_TRACE=1
  * in the environment): device timestamps (100 MHz wall clock) of the last
- * decode step: launch start, the moment every work-group had arrived at
- * each barrier (after the embedding, then per layer QKV, attention, [split
- * merge,] Wo, gate/up, down), and the end of the LM head.  Returns the count
- * written (0 when tracing is off). */
+ * decode step, out[0] when work-group 0 started and out[1] when it ended.
+ * Returns the count written (0 when tracing is off). */
 int cmolhip_persist_trace(cmolhip_model_t *m, uint64_t *out, int cap);
-/* Per-work-group phase times of the last step (same profiling mode):
- * out[stage][work-group][4] for stages 0..barriers: left the previous
- * barrier, operand and first weights staged (matvec stages), work done,
- * own stores drained.  Returns the work-group count, CMOL_ERR_TRUNC when
- * cap is too small. */
+/* Per-work-group stage times of the last step (same profiling mode):
+ * out[stage][work-group][8] for the stages embedding, then per layer QKV,
+ * attention, merge, Wo, gate/up, down, then the LM head: [0] the io waves
+ * start polling the stage's input, [1] the input is complete, [2] the
+ * stage's outputs are issued, [3] the mac waves start the stage's products,
+ * [4] their products are done, [5] their next weights are issued; [6] the
+ * work-group ends (last stage only) (0 where a work-group had no part).
+ * Returns the work-group count, CMOL_ERR_TRUNC when cap is too small. */
 int cmolhip_persist_marks(cmolhip_model_t *m, uint64_t *out, size_t cap);
 /* Lock-step decode of n sessions (distinct slots, each at its own pos).
  * logits_host: NULL or [n][vocab]. */

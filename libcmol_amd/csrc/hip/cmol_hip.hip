@@ -917,41 +917,48 @@ void plan_prefill(Plan &P, const cmolhip_model_desc_t *d)
 }
 
 
-// Attention splits of the persistent kernel's partial buffers.
-int persist_max_splits(int max_ctx) { return attn_max_splits(max_ctx, PK_CHUNK); }
+// Work-groups the persistent kernel will run with: one per CU of device 0
+// (at most PK_MAX_WGS; 256 when no device is visible, for size estimates).
+int persist_wgs()
+{
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || cus < 1) {
+        (void)hipGetLastError();
+        cus = 256;
+    }
+    return cus < PK_MAX_WGS ? cus : PK_MAX_WGS;
+}
 
-// CMOL_PERSIST_TRACE=1: the persistent kernel records when every
-// work-group has arrived at each barrier (profiling; see
-// cmolhip_persist_trace).
+// Attention splits of the persistent kernel: one item per work-group.
+int persist_max_splits(const cmolhip_hparams_t &h) { return persist_wgs() / h.n_kv_heads; }
+
+// CMOL_PERSIST_TRACE=1: the persistent kernel records per-stage times of
+// every work-group (profiling; see cmolhip_persist_marks).
 bool persist_tracing()
 {
     const char *e = getenv("CMOL_PERSIST_TRACE");
     return e && e[0] == '1';
 }
 
-// Trace entries of one launch: start, one per barrier (at most 6 per layer
-// + 1), end.
-int pk_trace_cap(const cmolhip_hparams_t &h) { return 6 * h.n_layers + 3; }
+// Exchange floats of one layer and parity (q, kn, vn, partials, att, xa, h, xo).
+size_t pk_ex_floats(const cmolhip_hparams_t &h)
+{
+    const size_t d = h.d_model, kvd = (size_t)h.n_kv_heads * h.d_head;
+    const size_t part = (size_t)h.n_heads * persist_max_splits(h) * (h.d_head + 4);
+    return d + 2 * kvd + part + 3 * d + h.d_ffn;
+}
 
 // Exchange buffers of the persistent kernel, in allocation order (mirrored
 // by build_persist).
 void plan_persist(Plan &P, const cmolhip_hparams_t &h)
 {
-    const size_t d = h.d_model, np = (size_t)h.n_heads * persist_max_splits(h.max_ctx);
-    for (int l = 0; l < h.n_layers; l++) {
-        for (int i = 0; i < 4; i++) P.add(d * 4);   // q, att, x_attn, x_ffn
-        P.add((size_t)h.d_ffn * 4);                 // h
-        P.add(np * 4);
-        P.add(np * 4);
-        P.add(np * h.d_head * 4);
-    }
-    P.add(d * 4);
+    P.add(((size_t)2 * h.d_model + (size_t)2 * h.n_layers * pk_ex_floats(h)) * 4);   // x0, then every layer
     P.add((size_t)h.n_layers * sizeof(PkLayer));
-    P.add((size_t)(16 * PK_MAX_WGS + 8 * 32) * 4);
-    P.add(4);
+    P.add(4);                                              // launch counter
+    P.add(4);                                              // error flag
     if (persist_tracing()) {
-        P.add((size_t)pk_trace_cap(h) * 8);
-        P.add((size_t)pk_trace_cap(h) * PK_MAX_WGS * 4 * 8);
+        P.add(2 * 8);
+        P.add((size_t)pk_stages(h.n_layers) * PK_MAX_WGS * PK_MARKS * 8);
     }
 }
 
@@ -1018,10 +1025,12 @@ struct cmolhip_model {
     std::mutex scratch_mu;
     bool use_graph = true;
     bool qk_norm = false;   // some layer normalises q or k per head
+    int max_fold = 1;       // largest fold of the model's tensors
     // persistent single-session decode (pk_dt = layer format, 0: not used)
     int pk_dt = 0, pk_nwg = 0, pk_lds = 0;
     PkArgs pk{};                  // launch arguments but the per-step fields
-    unsigned pk_epoch = 0;        // barrier epochs used so far
+    float *pk_ex = nullptr;       // exchange buffers of both parities
+    size_t pk_ex_n = 0;           // floats at pk_ex
     int *h_pk_err = nullptr;      // pinned copy of pk.err
     unsigned long long *h_trace = nullptr;   // pinned copy of the last step's stage times
     int trace_n = 0;
@@ -1436,6 +1445,17 @@ int launch_persist(int dt, const PkArgs &a, int nwg, int lds, hipStream_t s)
     }
 }
 
+// Every exchange buffer of both parities filled with PK_POISON, the launch
+// counter and error flag cleared (at creation, and after a launch whose wait
+// gave up).
+int persist_reset(cmolhip_model *m, hipStream_t st)
+{
+    HC(hipMemsetD32Async((hipDeviceptr_t)m->pk_ex, (int)PK_POISON, m->pk_ex_n, st));
+    HC(hipMemsetAsync(m->pk.tok, 0, 4, st));
+    HC(hipMemsetAsync(m->pk.err, 0, 4, st));
+    return E_OK;
+}
+
 // Exchange buffers and launch arguments of the persistent kernel (after the
 // weights and caches exist).  The kernel stays off (pk_dt = 0) when the
 // device cannot keep a work-group per CU resident with its LDS needs.
@@ -1443,13 +1463,22 @@ int build_persist(cmolhip_model *m, int dt)
 {
     cmolhip_ctx_t *c = m->ctx;
     const cmolhip_hparams_t &h = m->hp;
-    const size_t d = h.d_model, np = (size_t)h.n_heads * persist_max_splits(h.max_ctx);
+    const size_t d = h.d_model, kvd = (size_t)h.n_kv_heads * h.d_head, exn = pk_ex_floats(h);
+    const int ms = persist_max_splits(h);
     std::vector<PkLayer> ly(h.n_layers);
-    int lds = 0;
+    int opb = 0;
     auto need = [&](const cmolhip_qtensor_t &t) {
-        const int b = pk_gemv_lds(t.fold, t.block_quads);
-        lds = b > lds ? b : lds;
+        const int b = pk_op_bytes(t.fold, t.block_quads);
+        opb = b > opb ? b : opb;
     };
+    // the embedding rows of both parities, then every layer's exchange
+    // vectors: one block, filled with PK_POISON as a whole
+    float *ex = nullptr;
+    RC(arena_get(c, 2 * d + (size_t)2 * h.n_layers * exn, &ex));
+    m->pk_ex = ex;
+    m->pk_ex_n = 2 * d + (size_t)2 * h.n_layers * exn;
+    float *const x0 = ex;
+    ex += 2 * d;
     for (int l = 0; l < h.n_layers; l++) {
         const MLayer &L = m->layers[l];
         PkLayer &Y = ly[l];
@@ -1465,14 +1494,25 @@ int build_persist(cmolhip_model *m, int dt)
         Y.ffn_norm = L.ffn_norm;
         Y.rope_on = L.rope_on;
         Y.kv_off = (size_t)l * m->layer_stride;
-        RC(arena_get(c, d, &Y.q));
-        RC(arena_get(c, d, &Y.att));
-        RC(arena_get(c, d, &Y.x_attn));
-        RC(arena_get(c, d, &Y.x_ffn));
-        RC(arena_get(c, (size_t)h.d_ffn, &Y.h));
-        RC(arena_get(c, np, &Y.pm));
-        RC(arena_get(c, np, &Y.pl));
-        RC(arena_get(c, np * h.d_head, &Y.po));
+        for (int p = 0; p < 2; p++) {
+            float *b = ex + ((size_t)p * h.n_layers + l) * exn;
+            PkEx &E = Y.ex[p];
+            E.q = b;
+            b += d;
+            E.kn = b;
+            b += kvd;
+            E.vn = b;
+            b += kvd;
+            E.part = b;
+            b += (size_t)h.n_heads * ms * (h.d_head + 4);
+            E.att = b;
+            b += d;
+            E.xa = b;
+            b += d;
+            E.xo = b;
+            b += d;
+            E.h = b;
+        }
     }
     const cmolhip_qtensor_t &lm = lm_tensor(m);
     need(lm);
@@ -1482,7 +1522,7 @@ int build_persist(cmolhip_model *m, int dt)
     a.lm = to_qt(lm);
     a.out_norm = m->out_norm;
     a.rope = m->rope;
-    RC(arena_get(c, d, &a.x0));
+    a.x0 = x0;
     PkLayer *dl = nullptr;
     RC(cmolhip_alloc(c, ly.size() * sizeof(PkLayer), ALIGN, (void **)&dl));
     RC(cmolhip_memcpy_h2d(c, dl, ly.data(), ly.size() * sizeof(PkLayer)));
@@ -1494,23 +1534,37 @@ int build_persist(cmolhip_model *m, int dt)
     a.n_heads = h.n_heads;
     a.n_kv = h.n_kv_heads;
     a.d_head = h.d_head;
+    a.d_ffn = h.d_ffn;
     a.max_ctx = h.max_ctx;
     a.kv_f16 = h.kv_f16;
-    a.max_splits = persist_max_splits(h.max_ctx);
+    a.max_splits = ms;
+    a.op_bytes = opb;
     a.eps = h.rms_eps;
-    const size_t sync_bytes = (size_t)(16 * PK_MAX_WGS + 8 * 32) * 4;
-    RC(cmolhip_alloc(c, sync_bytes, ALIGN, (void **)&a.sync));
+    RC(cmolhip_alloc(c, 4, ALIGN, (void **)&a.tok));
     RC(cmolhip_alloc(c, 4, ALIGN, (void **)&a.err));
-    HC(hipMemsetAsync(a.sync, 0, sync_bytes, c->stream));
-    HC(hipMemsetAsync(a.err, 0, 4, c->stream));
+    RC(persist_reset(m, c->stream));
     HC(hipHostMalloc((void **)&m->h_pk_err, 4, hipHostMallocDefault));
     if (persist_tracing()) {
-        RC(arena_get(c, (size_t)pk_trace_cap(h), &a.trace));
-        RC(arena_get(c, (size_t)pk_trace_cap(h) * PK_MAX_WGS * 4, &a.marks));
-        HC(hipHostMalloc((void **)&m->h_trace, (size_t)pk_trace_cap(h) * 8, hipHostMallocDefault));
+        RC(arena_get(c, 2, &a.trace));
+        RC(arena_get(c, (size_t)pk_stages(h.n_layers) * PK_MAX_WGS * PK_MARKS, &a.marks));
+        HC(hipHostMalloc((void **)&m->h_trace, 2 * 8, hipHostMallocDefault));
     }
+    const int G = h.n_heads / h.n_kv_heads;
+    const int lds = pk_lds(opb, h.d_model, h.d_head, h.kv_f16, G, ms).total;
     const int nwg = persist_capacity(dt, h.d_head, h.kv_f16, lds);
-    if (nwg < 1 || a.max_splits > ATT_MAX_MERGE) return E_OK;   // stays off
+    // every work-group at most one attention item and one merge item; the io
+    // threads' operand share within PK_MAXI items
+    int max_tiles = 0;   // tiles of one matrix per mac wave (the LM head finishes its tiles in registers)
+    for (const PkLayer &Y : ly)
+        for (const QTensor *t : {&Y.qkv, &Y.o, &Y.gu, &Y.down}) {
+            const int w = PK_MAC * persist_wgs(), n = (t->row_tiles + w - 1) / w;
+            max_tiles = n > max_tiles ? n : max_tiles;
+        }
+    const bool fits = nwg == persist_wgs() && (size_t)ms * h.n_kv_heads <= (size_t)nwg && max_tiles <= PK_ZW_TILES &&
+                      h.n_heads * (h.d_head / PK_MSLICE) <= nwg && h.d_head % PK_MSLICE == 0 &&
+                      h.d_ffn / 8 <= PK_MAXI * 64 * PK_IO && h.d_model / 8 <= PK_MAXI * 64 * PK_IO &&
+                      ms * 9 <= 12 * 64 * PK_IO && G <= ATT_MAX_G;
+    if (nwg < 1 || !fits) return E_OK;   // stays off
     m->pk_dt = dt;
     m->pk_nwg = nwg;
     m->pk_lds = lds;
@@ -1526,33 +1580,24 @@ int run_persist(cmolhip_model *m, Batch &B)
     a.slot_id = B.slot_ids;
     a.logits = B.logits;
     a.argmax = B.argmax;
-    const int L = B.h_steps[2] < m->hp.max_ctx ? B.h_steps[2] : m->hp.max_ctx;
-    const unsigned nb = (unsigned)pk_barriers(L, m->hp.n_kv_heads, m->pk_nwg, m->hp.n_layers);
-    if (m->pk_epoch > 0x7fffffffu) {   // restart the epochs long before they wrap
-        HC(hipMemsetAsync(a.sync, 0, (size_t)(16 * PK_MAX_WGS + 8 * 32) * 4, B.st));
-        m->pk_epoch = 0;
-    }
-    a.epoch0 = m->pk_epoch;
     RC(launch_persist(m->pk_dt, a, m->pk_nwg, m->pk_lds, B.st));
-    m->pk_epoch += nb;
     HC(hipMemcpyAsync(m->h_pk_err, a.err, 4, hipMemcpyDeviceToHost, B.st));
     if (a.trace) {
-        m->trace_n = (int)nb + 2;
-        HC(hipMemcpyAsync(m->h_trace, a.trace, (size_t)m->trace_n * 8, hipMemcpyDeviceToHost, B.st));
+        m->trace_n = 2;
+        HC(hipMemcpyAsync(m->h_trace, a.trace, 2 * 8, hipMemcpyDeviceToHost, B.st));
     }
     return E_OK;
 }
 
-// After the step's synchronisation: a barrier wait that gave up leaves the
-// step's outputs invalid; the barrier state is reset for the next step.
+// After the step's synchronisation: a wait that gave up leaves the step's
+// outputs invalid and the exchange buffers in an unknown state; they are
+// poisoned again for the next step.
 int persist_check(cmolhip_model *m, Batch &B)
 {
     if (!*m->h_pk_err) return E_OK;
-    HC(hipMemsetAsync(m->pk.sync, 0, (size_t)(16 * PK_MAX_WGS + 8 * 32) * 4, B.st));
-    HC(hipMemsetAsync(m->pk.err, 0, 4, B.st));
+    RC(persist_reset(m, B.st));
     HC(hipStreamSynchronize(B.st));
     *m->h_pk_err = 0;
-    m->pk_epoch = 0;
     return E_UNSUPPORTED;
 }
 
@@ -1598,6 +1643,15 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
         RC(upload_q(c, 1, lh, CMOLHIP_PARTS_CONCAT, head_fold(d), stg, P.staging, &m->lm));
     }
     RC(upload_norm(c, d->out_norm, &m->out_norm));
+    auto fold_of = [&](const cmolhip_qtensor_t &t) { m->max_fold = t.fold > m->max_fold ? t.fold : m->max_fold; };
+    for (const MLayer &L : m->layers) {
+        for (int r = 0; r < L.n_qkv; r++) fold_of(L.qkv[r]);
+        fold_of(L.o);
+        fold_of(L.gu);
+        fold_of(L.down);
+    }
+    fold_of(m->embd);
+    if (m->lm.qs) fold_of(m->lm);
     const size_t rope_n = (size_t)h.max_ctx * (h.d_head / 2) * 2;
     RC(arena_get(c, rope_n, &m->rope));
     RC(cmolhip_memcpy_h2d(c, m->rope, d->rope_table, rope_n * 4));
@@ -1816,7 +1870,7 @@ int cmolhip_persist_marks(cmolhip_model_t *m, uint64_t *out, size_t cap)
 {
     if (!m || !out) return E_ARGS;
     if (!m->pk.marks || !m->trace_n) return 0;
-    const size_t n = (size_t)(m->trace_n - 1) * m->pk_nwg * 4;
+    const size_t n = (size_t)pk_stages(m->hp.n_layers) * m->pk_nwg * PK_MARKS;
     if (cap < n) return E_TRUNC;
     HC(hipMemcpy(out, m->pk.marks, n * 8, hipMemcpyDeviceToHost));
     return m->pk_nwg;
@@ -1839,7 +1893,10 @@ int cmolhip_prefill(cmolhip_model_t *m, int slot, const int32_t *tokens, int n, 
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->hp.vocab) return E_ARGS;
     if (n == 1) return cmolhip_decode(m, slot, tokens[0], pos0, logits_host, argmax);
-    if (n <= PROMPT_MATVEC_MAX) return prompt_by_matvec(m, slot, tokens, n, pos0, logits_host, argmax);
+    // a few tokens run as one lock-step matvec step (its MFMA rows hold
+    // 2 n fold <= 64 operand rows), longer prompts as GEMM passes
+    if (n <= PROMPT_MATVEC_MAX && n * m->max_fold <= 32)
+        return prompt_by_matvec(m, slot, tokens, n, pos0, logits_host, argmax);
     Batch &B = *m->slots[slot];
     Prefill &F = *m->pf;
     std::lock_guard<std::mutex> g(B.mu);

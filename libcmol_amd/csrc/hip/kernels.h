@@ -299,25 +299,48 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s);
 int attn_max_splits(int max_ctx, int split);
 
 // ---- persist_q4/q5/q8.hip: the persistent single-session decode kernel
+// One cooperative launch per token, one work-group of PK_THREADS per CU.
+// Waves 0..PK_IO-1 ("io waves") poll the vectors a stage consumes, stage
+// them into LDS, run attention's softmax bookkeeping and the split merge and
+// store those results; waves PK_IO.. ("mac waves") hold the weight rings,
+// prefetch weights and the KV tile ahead of need and run the matvecs.
+// Stages hand over fp32 vectors through exchange buffers that start each
+// launch filled with PK_POISON (a signalling-NaN pattern no arithmetic
+// produces): a reader waits until every element it needs differs from it.
+// The buffers are double-buffered by launch parity, and during a launch each
+// work-group refills the elements it writes with PK_POISON in the other
+// parity's (idle) buffers, ready for the next launch.
 #define PK_THREADS 512
 #define PK_WAVES (PK_THREADS / 64)
-#define PK_CHUNK (PK_THREADS / 4)   // attention positions per chunk
-#define PK_SPIN_MAX (1 << 18)       // polls of one barrier wait before it gives up
+#define PK_IO 4                     // io waves
+#define PK_MAC (PK_WAVES - PK_IO)   // mac waves
+#define PK_SPIN_MAX (1 << 16)       // poll rounds of one wait before it gives up
 #define PK_MAX_WGS 1024
+#define PK_POISON 0x7FBADBADu
+#define PK_KV_POS 64                // attention positions staged in LDS per chunk
+#define PK_MSLICE 32                // output dimensions per merge item
+#define PK_MAXI 8                   // (block, group) items per io thread: inputs <= 16384
+#define PK_ZW_TILES 64              // tiles of one matrix per mac wave (tile scratch)
+#define PK_MARKS 8                  // profiling marks per (stage, work-group)
 
-// Weights and exchange buffers of one layer (device copy, read-only).  The
-// stages hand each other plain fp32 vectors; every matvec stage builds its
-// own MFMA operand (and RMSNorm scale) from the vector it consumes.
+// Exchange vectors of one layer and launch parity.
+struct PkEx {
+    float *q;          // roped queries [d]
+    float *kn, *vn;    // this position's K and V rows [n_kv * d_head], as cached
+    float *part;       // attention split partials [n_heads][max_splits][d_head + 4]: o, m, l
+    float *att;        // attention output [d]
+    float *xa;         // residual after the attention block [d]
+    float *h;          // SwiGLU output [d_ffn]
+    float *xo;         // layer output [d]
+};
+
+// Weights of one layer and its exchange buffers (device copy, read-only).
 struct PkLayer {
     QTensor qkv, o, gu, down;
     const float *attn_norm, *ffn_norm;
     int rope_on;
-    size_t kv_off;                 // layer offset in the KV caches (elements)
-    float *q;                      // roped queries [d]
-    float *att;                    // attention output [d]
-    float *x_attn, *x_ffn;         // residual after the attention block / after the FFN [d]
-    float *h;                      // SwiGLU output [d_ffn]
-    float *pm, *pl, *po;           // attention split partials
+    size_t kv_off;     // layer offset in the KV caches (elements)
+    PkEx ex[2];
 };
 
 struct PkArgs {
@@ -325,46 +348,60 @@ struct PkArgs {
     int n_layers;
     QTensor embd, lm;
     const float *out_norm, *rope;
-    float *x0;                     // embedding row [d]
+    float *x0;                     // embedding rows [2][d], by parity
     float *logits;                 // [vocab]
     unsigned long long *argmax;    // [ARGMAX_SLOTS]
     void *k_base, *v_base;
     size_t slot_stride;
     const int32_t *slot_id;        // device [1]: the session's KV slot
     const int32_t *step;           // device {token, pos, seqlen}
-    int d, n_heads, n_kv, d_head, max_ctx, kv_f16, max_splits;
+    int d, n_heads, n_kv, d_head, d_ffn, max_ctx, kv_f16, max_splits;
+    int op_bytes;                  // LDS operand area (largest matrix operand + zero slot)
     float eps;
-    unsigned *sync;                // arrival words [PK_MAX_WGS][16], release words [8][32]
-    unsigned epoch0;               // barrier epochs of this launch are epoch0+1, epoch0+2, ...
-    int *err;                      // set when a barrier wait gave up
-    unsigned long long *trace;     // optional: [0] launch start, [i] all arrived at barrier i, then end
-    unsigned long long *marks;     // optional: [barrier i][work-group][4] phase times of stage i+1
+    unsigned *tok;                 // launches so far: this launch's parity is *tok & 1
+    int *err;                      // set when a wait gave up (the step's outputs are invalid)
+    unsigned long long *trace;     // optional: work-group 0's stage times
+    unsigned long long *marks;     // optional: [stage][work-group][PK_MARKS] phase times
 };
 
-// Positions per attention split for attended length L: multiples of the
-// chunk, enough splits to give every work-group an item.
-__host__ __device__ inline int pk_split(int L, int n_kv, int nwg)
+// Positions per attention split for attended length L (at most max_splits
+// splits, every work-group an item while there are positions for it).
+__host__ __device__ inline int pk_split(int L, int max_splits)
 {
-    const int want = (L * n_kv + nwg - 1) / nwg;
-    const int s = (want + PK_CHUNK - 1) / PK_CHUNK * PK_CHUNK;
-    return s < PK_CHUNK ? PK_CHUNK : s;
+    const int s = (L + max_splits - 1) / max_splits;
+    return s < 1 ? 1 : s;
 }
 
-// Barriers one launch passes: after the embedding, then per layer after the
-// QKV, attention, (merge,) Wo, gate/up and down stages.
-__host__ __device__ inline int pk_barriers(int L, int n_kv, int nwg, int n_layers)
-{
-    const int split = pk_split(L, n_kv, nwg);
-    const int nsplit = (L + split - 1) / split;
-    return 1 + n_layers * (5 + (nsplit > 1 ? 1 : 0));
-}
+// Stages one launch passes: the embedding, 6 per layer (QKV, attention,
+// merge, Wo, gate/up, down), the LM head.
+__host__ __device__ inline int pk_stages(int n_layers) { return 2 + 6 * n_layers; }
 
-// LDS bytes pk_gemv needs for a matrix (operand incl. padding blocks, a zero
-// slot, 16 floats of tile scratch per wave and the waves' sums of squares).
-__host__ __device__ inline int pk_gemv_lds(int fold, int block_quads)
+// LDS layout of the kernel (byte offsets).
+struct PkLds {
+    int op, kv, xr1, xr2, q, sc, red, ss, zw, ml, mrg, total;
+};
+__host__ __device__ inline PkLds pk_lds(int op_bytes, int d, int d_head, int kv_f16, int G, int max_splits)
 {
-    return 4 * fold * block_quads * 128 + 16 + PK_WAVES * 64 + PK_WAVES * 4;
+    PkLds L;
+    int o = 0;
+    auto take = [&](int bytes) { const int r = o; o += (bytes + 15) & ~15; return r; };
+    L.op = take(op_bytes);                                   // matvec operand (+ zero slot)
+    L.kv = take(2 * PK_KV_POS * d_head * (kv_f16 ? 2 : 4));   // K rows, then V rows
+    L.xr1 = take(4 * d);                                     // residual of the Wo stage (fp32)
+    L.xr2 = take(4 * d);                                     // residual of the down stage (fp32)
+    L.q = take(4 * G * d_head);                              // the item's queries; merge rows
+    L.sc = take(4 * G * PK_KV_POS);                          // scores / weights
+    L.red = take(4 * G * d_head);                            // attention output accumulators
+    L.ss = take(4 * 16);                                     // io waves' sums of squares, nrm
+    L.zw = take(4 * 16 * PK_ZW_TILES * PK_MAC);              // mac waves' tile scratch
+    L.ml = take(4 * 4 * 8);                                  // running max / sum / alpha per head
+    L.mrg = take(4 * max_splits * (PK_MSLICE + 2));          // merge: the splits' rows
+    L.total = o;
+    return L;
 }
+// LDS the matvec operand of a matrix needs (all k parts, padding blocks, a
+// zero slot).
+__host__ __device__ inline int pk_op_bytes(int fold, int block_quads) { return 4 * fold * block_quads * 128 + 16; }
 
 // Launch (cooperative, nwg work-groups, lds dynamic LDS bytes) for layer
 // format q4/q5/q8; 0, -4 unsupported shape, -5 launch failure.

@@ -1,6 +1,6 @@
 """The persistent single-session decode kernel (one cooperative launch per
-token, device-wide barriers between the stages) against the oracle and
-against the per-kernel decode graph of the same model."""
+token; each stage's readers poll the vectors they consume) against the
+oracle and against the per-kernel decode graph of the same model."""
 import os
 
 import numpy as np
