@@ -461,12 +461,15 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
 // Merge of the splits of one (query head, vector) by NT threads:
 // mx = max_s m_s, L = sum_s l_s e^(m_s - mx), out = sum_s o_s e^(m_s - mx) / L.
 // Thread (d, sg) sums the splits s = sg (mod SG) for dim d; the SG partial
-// sums meet in LDS in a fixed order.  Sessions whose length fits one split
-// were finished by attn_split.
+// sums meet in LDS in a fixed order.  Every load of the first NT splits'
+// (m, l) and of the thread's first MP o values is issued at once (one round
+// trip); longer merges read the rest in loops.  Sessions whose length fits
+// one split were finished by attn_split.
 template <int DH, int NT, typename M>
 __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n)
 {
     constexpr int SG = NT / DH;
+    constexpr int MP = 16;   // o values per thread loaded with the (m, l)
     const int tid = threadIdx.x;
     const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
     const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
@@ -477,15 +480,29 @@ __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n
     __shared__ float part[SG][DH];
     const size_t hb = (((size_t)n * a.n_kv + kvh) * a.max_splits) * G + h;   // + s * G
     const int w = tid >> 6, lane = tid & 63;
-    float mx = -INFINITY;
-    for (int s = tid; s < nact; s += NT) mx = fmaxf(mx, a.pm[hb + (size_t)s * G]);
+    const int d = tid % DH, sg = tid / DH;
+    const float m0 = tid < nact ? a.pm[hb + (size_t)tid * G] : -INFINITY;
+    const float l0 = tid < nact ? a.pl[hb + (size_t)tid * G] : 0.0f;
+    float ov[MP];
+#pragma unroll
+    for (int i = 0; i < MP; i++) {
+        const int s = sg + i * SG;
+        ov[i] = s < nact ? a.po[(hb + (size_t)s * G) * DH + d] : 0.0f;
+    }
+    float mx = m0;
+    for (int s = tid + NT; s < nact; s += NT) mx = fmaxf(mx, a.pm[hb + (size_t)s * G]);
     mx = wave_max(mx);
     if (lane == 0) rsh[w] = mx;
     __syncthreads();
     mx = rsh[0];
     for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, rsh[i]);
     float Ls = 0.0f;
-    for (int s = tid; s < nact; s += NT) {
+    if (tid < nact) {
+        const float e = expf(m0 - mx);
+        wsh[tid] = e;
+        Ls += l0 * e;
+    }
+    for (int s = tid + NT; s < nact; s += NT) {
         const float e = expf(a.pm[hb + (size_t)s * G] - mx);
         wsh[s] = e;
         Ls += a.pl[hb + (size_t)s * G] * e;
@@ -496,10 +513,12 @@ __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n
     __syncthreads();
     float Lt = 0.0f;
     for (int i = 0; i < NT / 64; i++) Lt += rsh[i];
-    const int d = tid % DH, sg = tid / DH;
     float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MP; i++)
+        if (sg + i * SG < nact) acc += ov[i] * wsh[sg + i * SG];
 #pragma unroll 8
-    for (int s = sg; s < nact; s += SG) acc += a.po[(hb + (size_t)s * G) * DH + d] * wsh[s];
+    for (int s = sg + MP * SG; s < nact; s += SG) acc += a.po[(hb + (size_t)s * G) * DH + d] * wsh[s];
     part[sg][d] = acc;
     __syncthreads();
     if (tid < DH) {
