@@ -10,17 +10,27 @@ Also reported on the same line:
   * the isolated Q4_0 matvecs 11008x2048 and 2048x11008 at batch 1 and 8 with
     64 rotating weight copies (defeating the 256 MB Infinity Cache), timed with
     HIP events on the stream they run on -> `roofline`;
-  * the oracle's (CPU restatement of the reference) single-thread decode of
-    the same model on a bounded sample -> `cpu_baseline`.
+  * the SmolLM2-135M-shaped Q8_0 single session (32-token prompt + 128 greedy
+    tokens, also as effective weight GB/s) and the SmolLM2-360M-shaped Q5_0
+    16-session lock-step decode (contexts uniform in 64..1024);
+  * the roofline kernel's HBM traffic from two rocprofv3 counter passes run
+    by this script (FETCH_SIZE, WRITE_SIZE, scaled by a copy of known size);
+  * the oracle's (CPU restatement of the reference) decode of the same
+    configurations on bounded samples, one session per thread as the
+    reference runs them -> `cpu_baseline`.
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes as C
 import json
 import math
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -205,6 +215,73 @@ def bench_decode_32(path, spec, sessions, steps, warmup, lo=512, hi=16384):
             "kv_bytes_per_step": kv_bytes}
 
 
+def kv_bytes(spec, ctx_sum, elem_bytes):
+    """Bytes of K and V one decode step reads over contexts summing to ctx_sum."""
+    return float(ctx_sum) * spec.n_layers * 2 * spec.n_kv_heads * spec.d_head * elem_bytes
+
+
+def with_roofline(r, step_bytes):
+    """Adds the step's algorithmic bytes and its fraction of the HBM peak."""
+    gbps = step_bytes / (r["ms_per_step"] * 1e-3) / 1e9
+    r.update(bytes_per_step=step_bytes, GBps=round(gbps, 1), frac_of_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
+    return r
+
+
+def bench_decode_small(steps=128, prompt_len=32):
+    """SmolLM2-135M-shaped Q8_0 model, one session: a seeded 32-token prompt,
+    then 128 greedy decode steps, timed (the same run once before, untimed).
+    Its 142.9 MB of weights fit the 256 MB Infinity Cache, so the rate is
+    reported as effective weight GB/s rather than against HBM."""
+    spec = synth.PRESETS["smollm2-135m-q8_0"]
+    path = synth.model_file(spec)
+    m = native.Model(path, max_ctx=prompt_len + steps + 8, max_sessions=1)
+    s = m.acquire()
+    prompt = synth.tokens(prompt_len, 42, spec.vocab)
+    wall = 0.0
+    for _ in range(2):
+        s.reset()
+        tok, _ = s.prefill(prompt)
+        hiprt.device_synchronize()
+        t0 = time.perf_counter()
+        pos = prompt_len
+        for _ in range(steps):
+            tok, _ = s.forward(tok, pos)
+            pos += 1
+        hiprt.device_synchronize()
+        wall = time.perf_counter() - t0
+    m.close()
+    wb = spec.weight_bytes_per_token()
+    r = {"model": "SmolLM2-135M-shaped Q8_0", "sessions": 1, "prompt": prompt_len, "new_tokens": steps,
+         "tok_s": steps / wall, "ms_per_step": wall * 1e3 / steps, "weight_bytes_per_token": wb,
+         "effective_weight_GBps": round(wb * steps / wall / 1e9, 1)}
+    return with_roofline(r, wb + kv_bytes(spec, prompt_len + steps / 2, 4))
+
+
+def bench_decode_16(steps=16, warmup=2, sessions=16, lo=64, hi=1024):
+    """SmolLM2-360M-shaped Q5_0 model, 16 sessions decoding in lock-step over
+    fp32 KV caches of lengths uniform in 64..1024 (synthetic contents)."""
+    spec = synth.PRESETS["smollm2-360m-q5_0"]
+    path = synth.model_file(spec)
+    lens = synth.uniform_lengths(sessions, lo, hi, seed=5)
+    m = native.Model(path, max_ctx=int(lens.max()) + warmup + steps + 8, max_sessions=sessions)
+    ss = [m.acquire() for _ in range(sessions)]
+    for i, s in enumerate(ss):
+        s.fill_kv(int(lens[i]), seed=200 + i)
+    toks = synth.tokens(sessions, 6, spec.vocab)
+    for _ in range(warmup):
+        toks = native.decode_batch(ss, toks)
+    hiprt.device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = native.decode_batch(ss, toks)
+    hiprt.device_synchronize()
+    wall = time.perf_counter() - t0
+    m.close()
+    r = {"model": "SmolLM2-360M-shaped Q5_0", "sessions": sessions, "tok_s": sessions * steps / wall,
+         "ms_per_step": wall * 1e3 / steps, "mean_ctx": float(np.mean(lens))}
+    return with_roofline(r, spec.weight_bytes_per_token() + kv_bytes(spec, np.sum(lens) + sessions * (warmup + steps / 2), 4))
+
+
 def bench_generate_concurrent(path, spec, sessions, new_tokens, lo=512, hi=16384):
     """The public path with one thread per session: `sessions` concurrent
     cmol_generate callers (greedy, token ids) over the same log-uniform
@@ -279,22 +356,152 @@ def copy_calibration(mb, reps=4):
     return {"copy_bytes": nbytes, "copies": reps}
 
 
-def cpu_baseline(path, spec, n_tokens):
-    """The oracle (reference arithmetic restated in C), one thread, decoding
-    n_tokens positions of the same model."""
+def cpu_cores():
+    """Host threads the CPU baselines use: the CPU share of one GPU (at most
+    16, and at most what OMP_NUM_THREADS allows)."""
+    n = os.cpu_count() or 1
+    e = os.environ.get("OMP_NUM_THREADS", "")
+    if e.isdigit() and int(e) > 0:
+        n = min(n, int(e))
+    return max(1, min(n, 16))
+
+
+def cpu_baseline(cores, c4_tokens=3):
+    """The oracle (the reference's arithmetic restated in C, AVX-512
+    accumulation order, `kind` "port") on bounded samples of each
+    configuration, one session per thread as the reference runs them
+    (min(sessions, cores) threads).  The top-level figure is the headline
+    configuration: SmolLM3-3B-shaped single-session decode at context 2048
+    (synthetic KV), the same context as the GPU figure."""
     from oracle import oracle as O
-    om = O.Model(path, max_ctx=n_tokens + 4, order=O.AVX512, nthreads=1)
-    toks = synth.tokens(n_tokens, 42, spec.vocab)
-    om.forward(int(toks[0]), 0)
+    out = {}
+    spec3 = synth.PRESETS["smollm3-3b-q4_0"]
+    path3 = synth.model_file(spec3)
+    # C4: one session at context 2048, one thread
+    S = O.Sessions(path3, [2048 + c4_tokens + 4])
+    S.fill_kv(0, 2048, seed=1)
+    S.step([1], [2048], 1)   # pages the weights in
+    el = sum(S.step([5 + i], [2049 + i], 1) for i in range(c4_tokens))
+    S.close()
+    out["c4_decode_1"] = {"value": c4_tokens / el, "unit": "tok/s", "cores": 1,
+                          "sample": f"{c4_tokens} decode steps at positions 2049.. over a synthetic "
+                                    "2048-position fp32 KV cache"}
+    # C5: 32 sessions at the GPU leg's log-uniform lengths, fp16-rounded KV
+    lens = synth.log_uniform_lengths(32, 512, 16384, seed=7).astype(int)
+    th = min(32, cores)
+    S = O.Sessions(path3, [int(L) + 2 for L in lens], kv_f16=True)
+    for i, L in enumerate(lens):
+        S.fill_kv(i, int(L), seed=100 + i)
+    el = S.step(synth.tokens(32, 5, spec3.vocab), lens, th)
+    S.close()
+    out["c5_decode_32"] = {"value": 32 / el, "unit": "tok/s", "cores": th,
+                           "sample": "one lock-step decode step of 32 sessions at contexts drawn "
+                                     "log-uniformly from 512 to 16384 (synthetic KV), "
+                                     f"{th} threads"}
+    # C1: SmolLM2-135M-shaped Q8_0, one session, 32-token prompt then 32 steps
+    spec1 = synth.PRESETS["smollm2-135m-q8_0"]
+    om = O.Model(synth.model_file(spec1), max_ctx=72, nthreads=1)
+    toks = synth.tokens(64, 42, spec1.vocab)
+    for p in range(32):
+        om.forward(int(toks[p]), p)
     t0 = time.perf_counter()
-    for p in range(1, n_tokens):
+    for p in range(32, 64):
         om.forward(int(toks[p]), p)
     el = time.perf_counter() - t0
     om.close()
-    return {"value": (n_tokens - 1) / el, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{n_tokens - 1} decode steps of the same SmolLM3-3B-shaped Q4_0 model "
-                      f"(single session, positions 1..{n_tokens - 1}), oracle in the reference's "
-                      f"AVX-512 accumulation order, 1 thread"}
+    wb1 = spec1.weight_bytes_per_token()
+    out["c1_decode_1"] = {"value": 32 / el, "unit": "tok/s", "cores": 1,
+                          "effective_weight_GBps": round(wb1 * 32 / el / 1e9, 2),
+                          "sample": "32 decode steps after a 32-token prompt"}
+    # C3: SmolLM2-360M-shaped Q5_0, 16 sessions at uniform lengths 64..1024
+    spec_3 = synth.PRESETS["smollm2-360m-q5_0"]
+    lens = synth.uniform_lengths(16, 64, 1024, seed=5).astype(int)
+    th = min(16, cores)
+    S = O.Sessions(synth.model_file(spec_3), [int(L) + 4 for L in lens])
+    for i, L in enumerate(lens):
+        S.fill_kv(i, int(L), seed=200 + i)
+    toks = synth.tokens(16, 6, spec_3.vocab)
+    S.step(toks, lens, th)
+    el = S.step(toks, lens + 1, th) + S.step(toks, lens + 2, th)
+    S.close()
+    out["c3_decode_16"] = {"value": 32 / el, "unit": "tok/s", "cores": th,
+                           "sample": f"two lock-step steps of 16 sessions, {th} threads"}
+    # C2: the Q4_0 FFN matvec 11008x2048, one thread, n = 1 and 8
+    rows, cols = 11008, 2048
+    w = synth.normal(rows * cols, seed=1234, stream=rows * 7 + cols, std=0.02)
+    raw = synth.quantize(synth.Q4_0, w).reshape(rows, -1)
+    x = np.random.default_rng(1).standard_normal((8, cols)).astype(np.float32)
+    c2 = {}
+    for n, reps in ((1, 8), (8, 2)):
+        b = np.ascontiguousarray(x[:n].T)   # [k][n]
+        O.matmul(raw, b, rows, cols, synth.Q4_0)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            O.matmul(raw, b, rows, cols, synth.Q4_0)
+        el = (time.perf_counter() - t0) / reps
+        c2[f"n{n}"] = {"ms_per_call": round(el * 1e3, 2), "GBps": round(q4_bytes(rows, cols, n) / el / 1e9, 2)}
+    out["c2_gemv_q4_11008x2048"] = dict(c2, cores=1)
+    head = out["c4_decode_1"]
+    return {"value": round(head["value"], 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": "SmolLM3-3B-shaped Q4_0 single session, " + head["sample"]
+                      + "; the oracle in the reference's AVX-512 accumulation order",
+            "configs": out}
+
+
+# ---- HBM traffic of the roofline kernel, measured in this run -----------------
+TRAFFIC_SHAPE = (11008, 2048)
+
+
+def traffic_child():
+    """Run under rocprofv3 by measure_traffic: a device-to-device copy of known
+    size (the calibration kernel), then the roofline matvec."""
+    copy_calibration(64, reps=4)
+    bench_matvec(TRAFFIC_SHAPE[0], TRAFFIC_SHAPE[1], 1, copies=32, launches=32)
+
+
+def pmc_pass(counter, workdir):
+    """One rocprofv3 counter pass over traffic_child: mean counter value (KiB)
+    per dispatch of the largest copy and of the matvec kernel."""
+    env = dict(os.environ, TMPDIR="/tmp")
+    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
+           "-d", workdir, "-o", counter, "--", sys.executable, os.path.join(ROOT, "bench.py"), "--traffic-child"]
+    subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, check=True)
+    path = None
+    for root, _, files in os.walk(workdir):
+        for f in files:
+            if f.startswith(counter) and f.endswith("counter_collection.csv"):
+                path = os.path.join(root, f)
+    copy, mv = {}, []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name, v = r["Kernel_Name"], float(r["Counter_Value"])
+            if name.startswith("__amd_rocclr_copyBuffer"):
+                g = int(r["Grid_Size"])
+                copy.setdefault(g, []).append(v)
+            elif name.startswith("void k_gemv<"):
+                mv.append(v)
+    big = copy[max(copy)]
+    return sum(big) / len(big), sum(mv) / len(mv)
+
+
+def measure_traffic():
+    """HBM bytes per launch of the roofline matvec: FETCH_SIZE and WRITE_SIZE
+    (two passes), each scaled by what it reads for the 64 MiB copy.  None when
+    rocprofv3 is unavailable or a pass fails."""
+    if not shutil.which("rocprofv3"):
+        return None
+    work = tempfile.mkdtemp(prefix="cmol_pmc_", dir="/tmp")
+    try:
+        cf, mf = pmc_pass("FETCH_SIZE", work)
+        cw, mw = pmc_pass("WRITE_SIZE", work)
+    except (subprocess.CalledProcessError, OSError, KeyError, ValueError, ZeroDivisionError, TypeError):
+        return None
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
+    copy_kib = 64 * 1024
+    fs, ws = copy_kib / cf, copy_kib / cw
+    return {"bytes": int((mf * fs + mw * ws) * 1024), "fetch_KiB": round(mf, 1), "write_KiB": round(mw, 1),
+            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
 
 
 def main():
@@ -307,13 +514,18 @@ def main():
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--generate-tokens", type=int, default=48)
-    ap.add_argument("--skip", default="", help="comma list of: decode,sampled,multi,generate,matvec,gemm,cpu")
+    ap.add_argument("--skip", default="",
+                    help="comma list of: decode,sampled,small,multi16,multi,generate,matvec,gemm,traffic,cpu")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--synthetic-context", type=int, default=0,
                     help="decode after filling the KV cache with this many synthetic positions "
                          "instead of a prefill (profiling runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run device-to-device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
+    if args.traffic_child:
+        traffic_child()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               f"(every configuration fits one MI355X; sessions shard by data parallelism)",
@@ -359,6 +571,16 @@ def main():
             r = bench_matvec(rows, cols, 2048, copies=2, launches=16, fold=1)
             log(json.dumps(r))
             gm.append(r)
+    c1 = None
+    if "small" not in skip:
+        log("SmolLM2-135M-shaped single-session decode")
+        c1 = bench_decode_small()
+        log(json.dumps(c1))
+    c3 = None
+    if "multi16" not in skip:
+        log("SmolLM2-360M-shaped 16-session decode")
+        c3 = bench_decode_16()
+        log(json.dumps(c3))
     d32 = None
     if "multi" not in skip:
         log("32-session decode")
@@ -369,10 +591,15 @@ def main():
         log("32 concurrent cmol_generate callers")
         g32 = bench_generate_concurrent(path, spec, args.sessions, args.generate_tokens)
         log(json.dumps(g32))
+    traffic = None
+    if mv and "traffic" not in skip:
+        log("roofline kernel traffic (two rocprofv3 counter passes)")
+        traffic = measure_traffic()
+        log(json.dumps(traffic))
     cpu = None
     if "cpu" not in skip:
         log("cpu baseline")
-        cpu = cpu_baseline(path, spec, args.cpu_tokens)
+        cpu = cpu_baseline(cpu_cores(), args.cpu_tokens)
         log(json.dumps(cpu))
 
     weight_bytes = spec.weight_bytes_per_token()
@@ -381,13 +608,21 @@ def main():
         r = mv[0]
         roof = {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(r["frac_of_peak"], 4),
-                "traffic": recorded_traffic("gemv_q4_11008x2048_traffic.txt"),
+                "traffic": traffic["bytes"] if traffic else recorded_traffic("gemv_q4_11008x2048_traffic.txt"),
+                "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes in this run, scaled by a 64 MiB "
+                                   "copy: " + json.dumps(traffic)) if traffic else
+                                  "profiles/gemv_q4_11008x2048_traffic.txt (no counter pass in this run)",
                 "kernel": "k_gemv<Q4_0> 11008x2048 n=1",
                 "bytes_per_launch": r["bytes_per_launch"],
                 "us_per_launch": round(r["us_per_launch"], 3)}
     if d1 is None:
-        print(json.dumps({"metric": METRIC, "matvec": mv, "gemm": gm, "roofline": roof}), flush=True)
+        print(json.dumps({"metric": METRIC, "matvec": mv, "gemm": gm, "roofline": roof, "decode_135m_1": c1,
+                          "decode_360m_16": c3, "decode_32": d32, "cpu_baseline": cpu}), flush=True)
         return
+    ctx1 = d1["context"] + args.warmup + args.steps / 2
+    with_roofline(d1, weight_bytes + kv_bytes(spec, ctx1, 4))
+    if d32:
+        with_roofline(d32, weight_bytes + d32["kv_bytes_per_step"])
     out = {
         "metric": METRIC,
         "value": round(d1["tok_s"], 2),
@@ -399,7 +634,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32 accumulate, hi/lo f16 operands",
         "data": "synthetic (seeded random weights ~N(0,0.02), seeded random prompt ids)",
         "config": {"workload": "SmolLM3-3B-shaped Q4_0 (Q8_0 tied embd/LM head), 1 session, "
                                + (f"greedy decode at a {args.synthetic_context}-position synthetic "
@@ -410,6 +645,8 @@ def main():
                    "effective_weight_GBps": round(weight_bytes * d1["tok_s"] / 1e9, 1)},
         "decode_1": d1,
         "sampled_1": s1,
+        "decode_135m_1": c1,
+        "decode_360m_16": c3,
         "decode_32": d32,
         "generate_32": g32,
         "matvec": mv,

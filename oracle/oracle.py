@@ -175,6 +175,87 @@ class Model:
         return k.reshape(shp), v.reshape(shp)
 
 
+class Sessions:
+    """One oracle model shared by several sessions (CPU baselines): the
+    reference's concurrency model, one session per thread (its
+    tests/test_threads.c:153-172), each forward single-threaded.  KV caches
+    are filled with a synthetic pattern up to each session's length."""
+
+    def __init__(self, path: str, max_ctxs, kv_f16: bool = False):
+        self.h = lib().o_model_load(path.encode(), AVX512, 1)
+        if not self.h:
+            raise RuntimeError(f"oracle failed to load {path}")
+        hp = np.zeros(11, np.int32); hf = np.zeros(2, np.float32)
+        lib().o_model_hparams(self.h, hp.ctypes.data, hf.ctypes.data)
+        self.n_layers, self.n_kv, self.d_head = int(hp[0]), int(hp[2]), int(hp[4])
+        self.max_ctxs = [int(c) for c in max_ctxs]
+        self.ss = []
+        for c in self.max_ctxs:
+            s = lib().o_sess_new(self.h, c)
+            if not s:
+                self.close()
+                raise MemoryError("oracle session")
+            lib().o_sess_kv_f16(s, int(kv_f16))
+            self.ss.append(s)
+
+    def fill_kv(self, i, n, seed=0):
+        """Positions 0..n-1 of session i (every layer) get a repeated seeded
+        pattern (the pages are written, so the attention reads real memory)."""
+        c = self.max_ctxs[i]
+        row = self.n_kv * self.d_head
+        pat = (np.random.default_rng(seed).standard_normal(1 << 14) * 0.5).astype(np.float32)
+        for get in (lib().o_sess_k, lib().o_sess_v):
+            buf = np.ctypeslib.as_array(C.cast(get(self.ss[i]), C.POINTER(C.c_float)),
+                                        (self.n_layers * c * row,)).reshape(self.n_layers, c * row)
+            flat = buf[:, :n * row]
+            reps = -(-flat.shape[1] // pat.size)
+            flat[:] = np.tile(pat, reps)[:flat.shape[1]]
+
+    def step(self, tokens, positions, threads):
+        """One forward of every session (token i at position i), sessions
+        spread over `threads` threads; returns the wall seconds."""
+        import threading
+        import time
+        nxt = [0]
+        lock = threading.Lock()
+        err = []
+
+        def work():
+            while True:
+                with lock:
+                    i = nxt[0]
+                    nxt[0] += 1
+                if i >= len(self.ss):
+                    return
+                if not lib().o_forward(self.h, self.ss[i], int(tokens[i]), int(positions[i])):
+                    err.append(i)
+
+        th = [threading.Thread(target=work) for _ in range(max(1, threads))]
+        t0 = time.perf_counter()
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        el = time.perf_counter() - t0
+        if err:
+            raise RuntimeError(f"oracle forward failed for sessions {err}")
+        return el
+
+    def close(self):
+        for s in getattr(self, "ss", []):
+            lib().o_sess_free(s)
+        self.ss = []
+        if getattr(self, "h", None):
+            lib().o_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 # ---- the reference itself, built from its sources (only where it exists) ----
 _r = None
 
