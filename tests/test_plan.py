@@ -34,6 +34,9 @@ SHAPES = [
      Q6_K, Q6_K),
     ("smollm2-135m q8_0", hparams(30, 576, 9, 3, 1536, 49152, 32), Q8_0, Q8_0, Q8_0, Q8_0, Q8_0, Q8_0, Q8_0,
      None),
+    # hidden 4096: the operand slice of every projection is split in k
+    ("hidden-4096 q4_k_m", hparams(4, 4096, 32, 8, 14336, 32000, 32), Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q6_K,
+     Q6_K, Q6_K),
 ]
 
 
