@@ -275,8 +275,15 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
 // EPI >= 0 fixes the epilogue at compile time (the decode kernels: one
 // straight code path, so that a launch's cold instruction cache fetches
 // little); EPI < 0 takes it from sh.epi.
+//
+// The four-wave Q4_0 decode instances with a four-deep ring fit 80 VGPRs
+// without spilling and are held there (six waves per SIMD, six work-groups
+// per CU): pick_nw gives them matrices with more tiles than eight-wave
+// groups can keep resident at once.
 template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI>
-__global__ __launch_bounds__(NW * 64) void k_gemv(GemvArgs a, GemvShape sh)
+__global__ __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(DT == DT_Q4_0 && NW == 4 && NG == 1 && U == 4 && EPI != EPI_QKV ? 6 : 1)))
+void k_gemv(GemvArgs a, GemvShape sh)
 {
     // launch arguments needed before the weight loads go out, fetched in
     // one round trip
@@ -512,10 +519,28 @@ static inline int gb_env_int(const char *name, int def)
     return v < 1 ? 1 : v;
 }
 
-static inline int pick_nw(int tiles, int quads)
+// Compute units of the current device (cached: one device type per process).
+static inline int gemv_cus()
+{
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        return n > 0 ? n : 256;
+    }();
+    return cus;
+}
+
+static inline int pick_nw(int tiles, int quads, bool four_held)
 {
     static const int t16 = gb_env_int("CMOL_NW16_BELOW", 128), t8 = gb_env_int("CMOL_NW8_BELOW", 4096);   // measurements
     int nw = tiles < t16 ? 16 : tiles < t8 ? 8 : 4;
+    // eight-wave groups keep 4 per CU resident (32 waves): a matrix with more
+    // tiles runs a second round of work-groups, each as long as the first;
+    // four-wave groups held to six per CU (four_held) finish it in one
+    // (SmolLM3-3B gate/up, 1376 tiles: 10.3 us in two rounds)
+    if (four_held && nw == 8 && tiles > 4 * gemv_cus() && tiles <= 6 * gemv_cus() && quads >= 13 && quads <= 16)
+        nw = 4;
     if (const char *e = getenv("CMOL_GEMV_NW")) nw = atoi(e);
     static const int minq = [] {
         const char *e = getenv("CMOL_GEMV_MINQ");   // measurements
@@ -633,7 +658,7 @@ static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
 template <int DT, int NG>
 static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
 {
-    int nw = pick_nw(a.w.row_tiles, a.w.block_quads);
+    int nw = pick_nw(a.w.row_tiles, a.w.block_quads, DT == DT_Q4_0 && NG == 1);
     for (;; nw >>= 1) {
         GemvShape sh;
         bool ch;
