@@ -138,8 +138,9 @@ int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a,
  * fp32 or fp16 caches are stacked as [n][n_kv][max_ctx][d_head]; q is
  * [n][n_heads*d_head] after RoPE, seqlen[n] (device int32) the number of
  * positions attended, out [n][n_heads*d_head].  Each work-group covers
- * `split` positions (a multiple of 64; 0 picks 64) and splits are merged
- * with log-sum-exp rescaling.  Device pointers. */
+ * `split` positions (a multiple of 64, or of 32 for d_head 64 / 128; 0
+ * picks 64) and splits are merged with log-sum-exp rescaling.  Device
+ * pointers. */
 int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q,
                         const void *kcache, const void *vcache,
                         const int32_t *seqlen, int n_heads, int n_kv,

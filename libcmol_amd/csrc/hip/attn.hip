@@ -24,7 +24,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
 
 // Head-per-wave decode attention for d_head 64 and 128: one work-group of
 // four waves per (kv head, split, vector); wave w serves query heads w and
-// w + 4 of the group.  The split is walked in chunks of 64 positions whose
+// w + 4 of the group.  The split is walked in chunks of CH (32 or 64) positions whose
 // K and V rows are staged in LDS by all 256 threads (coalesced 16-byte
 // loads of the next chunk are in flight while the current one is used):
 //   * scores: four lanes per position, each holding a quarter of the head's
@@ -36,7 +36,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
 //     broadcast with readlane and its V row read once per wave.
 // Same partial format as attn_split, merged by k_attn_merge.
 #define ATH_CH 64
-template <int DH, typename KT>
+template <int DH, typename KT, int CH>
 __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
 {
 #pragma clang fp contract(off)
@@ -45,11 +45,12 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     constexpr int PE = 16 / (int)sizeof(KT);         // elements per 16-byte piece
     constexpr int NPL = RB / 16 / 4;                 // pieces per lane (a quarter of the row)
     constexpr int DL = DH / 64;                      // output dims per lane
-    constexpr int UNITS = ATH_CH * RB / 16;          // 16-byte units of a chunk's K (and of V)
+    constexpr int UNITS = CH * RB / 16;              // 16-byte units of a chunk's K (and of V)
     constexpr int UPT = UNITS / 256;                 // per thread
-    static_assert(UNITS % 256 == 0, "chunk size");
-    __shared__ __attribute__((aligned(16))) uint8_t ks[2][ATH_CH * KS];
-    __shared__ __attribute__((aligned(16))) uint8_t vs[2][ATH_CH * RB];
+    constexpr int PS = CH / 16;                      // 16-position passes per chunk
+    static_assert(UNITS % 256 == 0 && CH % 16 == 0, "chunk size");
+    __shared__ __attribute__((aligned(16))) uint8_t ks[2][CH * KS];
+    __shared__ __attribute__((aligned(16))) uint8_t vs[2][CH * RB];
 
     const int kvh = blockIdx.x, sp = blockIdx.y, n = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     const int t0 = sp * a.split;
     if (t0 >= L) return;
     const int cnt = min(L, t0 + a.split) - t0;
-    const int nch = (cnt + ATH_CH - 1) / ATH_CH;
+    const int nch = (cnt + CH - 1) / CH;
     const int nact = (L + a.split - 1) / a.split;
     const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
     const uint8_t *kb = (const uint8_t *)((const KT *)a.kv.k_base + off);
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u, row = unit / (RB / 16), col = unit % (RB / 16);
-            const size_t src = (size_t)min(c * ATH_CH + row, cnt - 1) * RB + col * 16;
+            const size_t src = (size_t)min(c * CH + row, cnt - 1) * RB + col * 16;
             kr[u] = ldg((const u32x4 *)(kb + src));
             vr[u] = ldg((const u32x4 *)(vb + src));
         }
@@ -112,14 +113,14 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
         if (c + 1 < nch) fetch(c + 1);
-        const int np = min(ATH_CH, cnt - c * ATH_CH);
+        const int np = min(CH, cnt - c * CH);
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             if (hh >= nh) break;
             // scores: pass ps covers positions 16 ps + lane/4
-            float sc[4];
+            float sc[PS];
 #pragma unroll
-            for (int ps = 0; ps < 4; ps++) {
+            for (int ps = 0; ps < PS; ps++) {
                 const uint8_t *kr0 = &ks[buf][(16 * ps + (lane >> 2)) * KS];
                 float dot = 0.0f;
 #pragma unroll
@@ -142,12 +143,14 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
                 dot += __shfl_xor(dot, 2, 64);
                 sc[ps] = (16 * ps + (lane >> 2)) < np ? dot * scale : -INFINITY;
             }
-            float mc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            float mc = sc[0];
+#pragma unroll
+            for (int ps = 1; ps < PS; ps++) mc = fmaxf(mc, sc[ps]);
             mc = wave_max(mc);
             const float mn = fmaxf(m[hh], mc);
-            float ev[4], ls = 0.0f;
+            float ev[PS], ls = 0.0f;
 #pragma unroll
-            for (int ps = 0; ps < 4; ps++) {
+            for (int ps = 0; ps < PS; ps++) {
                 ev[ps] = expf(sc[ps] - mn);
                 if (j == 0) ls += ev[ps];
             }
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
             for (int d = 0; d < DL; d++) o[hh][d] *= al;
             // weighted sum: lane covers dims DL*lane ..
 #pragma unroll
-            for (int ps = 0; ps < 4; ps++) {
+            for (int ps = 0; ps < PS; ps++) {
 #pragma unroll 4
                 for (int r = 0; r < 16; r++) {
                     const float ep = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[ps]), 4 * r));
@@ -543,20 +546,29 @@ int attn_max_splits(int max_ctx, int split) { return (max_ctx + split - 1) / spl
 int launch_attn(const AttnArgs &a, hipStream_t s)
 {
     const int G = a.n_heads / a.n_kv;
-    if (G < 1 || G > ATT_MAX_G || a.n_heads % a.n_kv || a.split < 1 || a.split % ATT_CHUNK)
+    // splits of whole 64-position chunks, or (head-per-wave kernel, d_head
+    // 64 / 128) of whole 32-position chunks
+    const bool half_chunks = a.split % ATT_CHUNK != 0;
+    if (G < 1 || G > ATT_MAX_G || a.n_heads % a.n_kv || a.split < 1 || a.split % (ATT_CHUNK / 2) ||
+        (half_chunks && a.d_head != 64 && a.d_head != 128))
         return -4;
     if (a.max_splits > ATT_MAX_MERGE) return -4;
     dim3 grid(a.n_kv, a.max_splits, a.n), block(ATT_THREADS), mgrid(a.n_heads, a.n);
 #define ATT(DHV)                                                                          \
     if (a.kv_f16) hipLaunchKernelGGL((k_attn<DHV, _Float16>), grid, block, 0, s, a);      \
     else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);
-#define ATH(DHV)                                                                          \
-    if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16>), grid, block, 0, s, a);    \
-    else hipLaunchKernelGGL((k_attn_h<DHV, float>), grid, block, 0, s, a);
+#define ATH(DHV)                                                                                  \
+    if (half_chunks) {                                                                            \
+        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, 32>), grid, block, 0, s, a);    \
+        else hipLaunchKernelGGL((k_attn_h<DHV, float, 32>), grid, block, 0, s, a);               \
+    } else {                                                                                      \
+        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, ATH_CH>), grid, block, 0, s, a); \
+        else hipLaunchKernelGGL((k_attn_h<DHV, float, ATH_CH>), grid, block, 0, s, a);           \
+    }
     // head-per-wave kernel for short splits (one or two chunks); the
     // thread-per-dimension kernel streams long splits better
     const char *e = getenv("CMOL_ATTN_H");
-    const bool head_waves = e ? e[0] == '1' : a.split <= 2 * ATH_CH;
+    const bool head_waves = half_chunks || (e ? e[0] == '1' : a.split <= 2 * ATH_CH);
     switch (a.d_head) {
     case 16: ATT(16); break;
     case 32: ATT(32); break;

@@ -459,7 +459,8 @@ int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kca
                         int max_ctx, int kv_f16, int split, float *out)
 {
     if (!c || n < 1 || !q || !kcache || !vcache || !seqlen || !out || n_kv < 1 || n_heads < n_kv ||
-        n_heads % n_kv || max_ctx < 1 || split < 0 || split % 64)
+        n_heads % n_kv || max_ctx < 1 || split < 0 || split % 32 ||
+        (split % 64 && d_head != 64 && d_head != 128))
         return E_ARGS;
     if (!split) split = 64;
     const int G = n_heads / n_kv, ms = attn_max_splits(max_ctx, split);
