@@ -6,10 +6,11 @@
 // form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31 (A rows
 // 64wm.. of the hi/lo operand, four 16-row MFMA groups) and output rows
 // 32wn..32wn+31 (two 16-row "virtual tiles").  The k loop walks block quads
-// through a three-stage pipeline: the activation operand of quad kk+2 is
+// through a two-stage pipeline: the activation operand of quad kk+1 is
 // copied into LDS with direct-to-LDS loads and each wave loads the weight
 // codes of its two virtual tiles for it into registers while quad kk is
-// contracted.  Weights of any fold are read in
+// contracted.  Two stages (64 KiB of LDS) keep two work-groups on a CU,
+// which hides more latency than a third stage in flight with one.  Weights of any fold are read in
 // place: virtual tile V of part p gathers, for column c', the codes of row
 // 16V + c' from tile (16V + c') / R, column p*R + c' % R.
 //
@@ -21,7 +22,7 @@
 
 #define GEMM_BM 64    // vectors per work-group
 #define GEMM_BN 128   // output rows per work-group (8 virtual tiles)
-#define GEMM_STAGES 3 // quads in flight
+#define GEMM_STAGES 2 // quads in flight
 #define GEMM_WAVES 8
 
 struct GemmShape {
@@ -105,7 +106,6 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
             q_load<DT>(a.w, cell, col, col + 16 * g, c0[st][j], c1[st][j], dv[st][j], hv[st][j]);
         }
     };
-    constexpr int LPS = 4 + 2 * q_loads<DT>();
 
     const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc[4][2];
@@ -140,13 +140,11 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
         }
     };
 
-    // three-stage k loop: at the top of step kk the loads of kk and kk+1 are
-    // outstanding; waiting for all but the newest stage's loads (they retire
-    // in issue order) leaves kk+1 in flight, the barrier publishes every
-    // wave's copy of kk, and kk+2 is issued into the stage kk-1 freed
+    // two-stage k loop: at the top of step kk only the loads of kk are
+    // outstanding; the wait and the barrier publish every wave's copy of kk
+    // (and every wave is done with kk-1), then kk+1 is issued into the stage
+    // kk-1 freed
     load_stage(0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_stage(1, 1);
     __builtin_amdgcn_sched_barrier(0);
     // the body is unconditional (steps past the end compute nothing and
     // re-read the last quad) so every wait count is the same on each pass
@@ -154,10 +152,10 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
 #pragma unroll
         for (int u = 0; u < GEMM_STAGES; u++) {
             const int kk = k0 + u;
-            __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(LPS));
+            __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
-            load_stage((u + 2) % GEMM_STAGES, kk + 2);
+            load_stage((u + 1) % GEMM_STAGES, kk + 1);
             __builtin_amdgcn_sched_barrier(0);
             compute(u, kk);
         }
