@@ -10,9 +10,10 @@
 // copied into LDS with direct-to-LDS loads and each wave loads the weight
 // codes of its two virtual tiles for it into registers while quad kk is
 // contracted.  Two stages (64 KiB of LDS) keep two work-groups on a CU,
-// which hides more latency than a third stage in flight with one.  Weights of any fold are read in
-// place: virtual tile V of part p gathers, for column c', the codes of row
-// 16V + c' from tile (16V + c') / R, column p*R + c' % R.
+// which hides more latency than a third stage in flight with one.
+// Weights of any fold are read in place: virtual tile V of part p gathers,
+// for column c', the codes of row 16V + c' from tile (16V + c') / R,
+// column p*R + c' % R.
 //
 // Arithmetic is the decode matvec's (gemv_impl.h): codes decoded to exact
 // f16 integers, v_mfma_f32_16x16x32_f16 against the exact hi/lo operand,
