@@ -121,13 +121,16 @@ def bench_matvec(rows, cols, n, copies, launches, fold=None, dtype=synth.Q4_0):
     return out
 
 
-def bench_decode_1(path, spec, prompt_len, steps, warmup, synthetic_ctx=0):
+def bench_decode_1(path, spec, prompt_len, steps, warmup, synthetic_ctx=0, prefill_chunk=0):
     """Single-session greedy decode after a prompt_len-token prefill, or (with
     synthetic_ctx > 0) after filling the KV cache with that many synthetic
-    positions instead of running a prefill."""
+    positions instead of running a prefill.  The prompt goes through the
+    prompt GEMMs in passes of prefill_chunk tokens (0: the whole prompt in
+    one pass, M = prompt_len)."""
     ctx_len = synthetic_ctx or prompt_len
     max_ctx = ctx_len + warmup + steps + 8
-    m = native.Model(path, max_ctx=max_ctx, max_sessions=1)
+    chunk = prefill_chunk or max(prompt_len, 1)
+    m = native.Model(path, max_ctx=max_ctx, max_sessions=1, prefill_chunk=chunk)
     s = m.acquire()
     t0 = time.perf_counter()
     if synthetic_ctx:
@@ -158,7 +161,7 @@ def bench_decode_1(path, spec, prompt_len, steps, warmup, synthetic_ctx=0):
     out = {"tok_s": steps / wall, "ms_per_step": wall * 1e3 / steps,
            "device_ms_per_step": dev_ms / steps, "context": ctx_len}
     if not synthetic_ctx:
-        out.update(prefill_tok_s=prompt_len / prefill_s, prefill_s=prefill_s)
+        out.update(prefill_tok_s=prompt_len / prefill_s, prefill_s=prefill_s, prefill_chunk=chunk)
     return out
 
 
@@ -510,6 +513,8 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--prefill-chunk", type=int, default=0,
+                    help="prompt tokens per prefill pass (default: the whole prompt, M = --prompt)")
     ap.add_argument("--sessions", type=int, default=32)
     ap.add_argument("--multi-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
@@ -542,7 +547,8 @@ def main():
     d1 = None
     if "decode" not in skip:
         log("single-session decode")
-        d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup, args.synthetic_context)
+        d1 = bench_decode_1(path, spec, args.prompt, args.steps, args.warmup, args.synthetic_context,
+                            args.prefill_chunk)
         log(json.dumps(d1))
     s1 = None
     if "sampled" not in skip:
