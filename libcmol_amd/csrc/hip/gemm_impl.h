@@ -31,6 +31,8 @@ struct GemmShape {
     int mt;          // 64-vector tiles
     int nt;          // 128-row tiles
     int vt;          // 16-row virtual tiles (ceil(rows / 16))
+    int ga;          // XCD slices along the vector tiles (1, 2, 4, 8)
+    int mts, nts;    // vector / row tiles per slice
 };
 
 template <int DT>
@@ -41,12 +43,14 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
     uint8_t *s_a = smem;                                 // GEMM_STAGES x ASTAGE
     float *s_nrm = (float *)(smem + GEMM_STAGES * ASTAGE);
 
-    // XCD-aware tile order: work-groups b, b+8, b+16, ... share an XCD; give
-    // them the same row tile so its weights are fetched into one L2
-    const int b = blockIdx.x;
-    const int grp = b / (8 * sh.mt);
-    const int nt_ = grp * 8 + (b & 7), mt_ = (b >> 3) % sh.mt;
-    if (nt_ >= sh.nt) return;
+    // XCD-aware tile order: work-groups b, b+8, b+16, ... share an XCD.  The
+    // (vector tile, row tile) grid is cut into ga x (8 / ga) slices, one per
+    // XCD; an XCD walks its slice vector tile fastest, so the operand tiles
+    // of its slice stay in its L2 while the weights stream past
+    const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
+    const int mt_ = (xcd % sh.ga) * sh.mts + i % sh.mts;
+    const int nt_ = (xcd / sh.ga) * sh.nts + i / sh.mts;
+    if (mt_ >= sh.mt || nt_ >= sh.nt) return;
     const int m0 = mt_ * GEMM_BM;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, cl = l & 15;
@@ -200,8 +204,13 @@ int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
     sh.mt = (a.n + GEMM_BM - 1) / GEMM_BM;
     sh.vt = (a.w.rows + 15) / 16;
     sh.nt = (sh.vt + 7) / 8;
-    const long groups = (sh.nt + 7) / 8;
-    const long wgs = groups * 8 * sh.mt;
+    // one slice of vector tiles per XCD (at M = 2048: 512 KiB of operand
+    // per vector tile, four per XCD) unless there are fewer vector tiles
+    sh.ga = 8;
+    while (sh.ga > 1 && sh.ga > sh.mt) sh.ga >>= 1;
+    sh.mts = (sh.mt + sh.ga - 1) / sh.ga;
+    sh.nts = (sh.nt + 8 / sh.ga - 1) / (8 / sh.ga);
+    const long wgs = 8L * sh.mts * sh.nts;
     if (wgs > 0x7fffffffL) return -6;
     const size_t lds = (size_t)GEMM_STAGES * 4 * 4 * 2 * GEMM_BM * 16 + GEMM_BM * 4;
     if (a.ev_start)
