@@ -35,6 +35,67 @@ struct GemmShape {
     int mts, nts;    // vector / row tiles per slice
 };
 
+// acc += the block's contribution for 16 vectors: xh holds their high
+// operand parts, xl their low parts (scaled by LO_SCALE), wv the decoded
+// codes and wl the codes times LO_INV_SCALE (exact: a power of two).  The
+// low products go into the same fp32 sum as the high ones, so one scale FMA
+// per output and block applies the block's factor to both.
+template <int DT>
+__device__ __forceinline__ void mfma_block_hl(f32x4 &acc, const f16x8 &xh, const f16x8 &xl, const f16x8 &wv,
+                                              const f16x8 &wl, const BlockScale &s)
+{
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (DT == DT_Q4_K) {
+        const _Float16 o = (_Float16)1, ol = (_Float16)LO_INV_SCALE;
+        const f16x8 ones = {o, o, o, o, o, o, o, o};
+        const f16x8 onesl = {ol, ol, ol, ol, ol, ol, ol, ol};
+        f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wv, z, 0, 0, 0);
+        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wl, cc, 0, 0, 0);
+        f32x4 cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, ones, z, 0, 0, 0);
+        cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, onesl, cs, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(s.s1, cs[i], fmaf(s.s0, cc[i], acc[i]));
+    } else if constexpr (DT == DT_Q6_K) {
+        const _Float16 o = (_Float16)0;
+        const f16x8 w0 = {wv[0], wv[1], wv[2], wv[3], o, o, o, o};
+        const f16x8 w1 = {o, o, o, o, wv[4], wv[5], wv[6], wv[7]};
+        const f16x8 l0 = {wl[0], wl[1], wl[2], wl[3], o, o, o, o};
+        const f16x8 l1 = {o, o, o, o, wl[4], wl[5], wl[6], wl[7]};
+        f32x4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, w0, z, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, l0, c0, 0, 0, 0);
+        f32x4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, w1, z, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, l1, c1, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(s.s1, c1[i], fmaf(s.s0, c0[i], acc[i]));
+    } else {
+        f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wv, z, 0, 0, 0);
+        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wl, cc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(s.s0, cc[i], acc[i]);
+    }
+}
+
+// q_load with precomputed element offsets: e = cell * 64 + lane (codes,
+// Q5_0 fifth bits, Q6_K high bits) and ds = the scale record's index
+// (cell * 64 + col * 4 halves, or cell * 16 + col K-quant records).
+template <int DT>
+__device__ __forceinline__ void gemm_wload(const QTensor &w, uint32_t e, uint32_t ds, u32x4 &c0, u32x4 &c1,
+                                           typename QScale<DT>::T &sv, uint32_t &h)
+{
+    constexpr uint32_t LB = QFmt<DT>::LANE_BYTES;
+    const u32x4 *p = (const u32x4 *)(w.qs + e * LB);
+    c0 = p[0];
+    if constexpr (DT == DT_Q8_0) c1 = p[1];
+    else if constexpr (DT == DT_Q6_K) {
+        const u32x2 hb = *(const u32x2 *)((const uint8_t *)w.qh + e * 8u);
+        c1 = u32x4{hb[0], hb[1], 0u, 0u};
+    } else c1 = u32x4{0, 0, 0, 0};
+    if constexpr (is_kquant(DT)) sv = *(const u32x4 *)((const uint8_t *)w.d + ds * 16u);
+    else sv = *(const u32x2 *)((const uint8_t *)w.d + ds * 2u);
+    if constexpr (DT == DT_Q5_0) h = *(const uint32_t *)((const uint8_t *)w.qh + e * 4u);
+    else h = 0u;
+}
+
 template <int DT>
 __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape sh)
 {
@@ -72,14 +133,26 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
         }
     }
 
-    // weight gather for this lane: virtual tile V -> (tile, column)
-    int wt[2], wc[2];
+    // weight gather for this lane: virtual tile V -> (tile, column).  The
+    // lane's element offsets within the tensor (32-bit: the host checks the
+    // size) are fixed here; each quad adds a uniform part
+    uint32_t wq[2], wd[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int V = nt_ * 8 + wn * 2 + j;
         const int row = V * 16 + cl;
-        wt[j] = min(row / R, a.w.row_tiles - 1);
-        wc[j] = row % R;   // + part * R
+        const uint32_t wt = (uint32_t)min(row / R, a.w.row_tiles - 1), wc = (uint32_t)(row % R);
+        wq[j] = wt * (uint32_t)BQ * 64u + wc + 16u * (uint32_t)g;   // cell * 64 + lane
+        wd[j] = is_kquant(DT) ? wt * (uint32_t)BQ * 16u + wc : wt * (uint32_t)BQ * 64u + 4u * wc;
+    }
+    // operand rows of this lane's two 64-row halves (LDS rows of each 32-row
+    // group: the 16 high parts, then the 16 low parts of its 16 vectors,
+    // operand rows 2v and 2v+1)
+    uint32_t arow[2];
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        const int l5 = l & 31;
+        arow[half] = 16u * (uint32_t)min(2 * m0 + 64 * half + (l & 32) + 2 * (l5 & 15) + (l5 >> 4), nrows - 1);
     }
 
     u32x4 c0[GEMM_STAGES][2], c1[GEMM_STAGES][2];
@@ -96,28 +169,25 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int s = wid * 4 + i;            // 16 (block, group) segments x 2 halves
-            const int seg = s >> 1, half = s & 1;
+            const int seg = s >> 1, half = i & 1;
             const int bi = seg >> 2, gg = seg & 3;
             const int blk = min(b0 + bi, nblk - 1);
-            const int r = min(2 * m0 + 64 * half + l, nrows - 1);
-            const uint8_t *src = (const uint8_t *)a.in.q + ((((size_t)blk * 4 + gg) * nrows) + r) * 16;
+            const uint8_t *src = (const uint8_t *)a.in.q + ((size_t)blk * 4 + gg) * nrows * 16 + arow[half];
             uint8_t *dst = s_a + st * ASTAGE + ((bi * 4 + gg) * 2 * GEMM_BM + 64 * half) * 16;
             __builtin_amdgcn_global_load_lds((const gvoid_t *)src, (lvoid_t *)dst, 16, 0, 0);
         }
+        const uint32_t uq = (uint32_t)(q * 64 + p * R);
+        const uint32_t ud = is_kquant(DT) ? (uint32_t)(q * 16 + p * R) : (uint32_t)(q * 64 + 4 * p * R);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const size_t cell = (size_t)wt[j] * BQ + q;
-            const int col = p * R + wc[j];
-            q_load<DT>(a.w, cell, col, col + 16 * g, c0[st][j], c1[st][j], dv[st][j], hv[st][j]);
-        }
+        for (int j = 0; j < 2; j++) gemm_wload<DT>(a.w, wq[j] + uq, wd[j] + ud, c0[st][j], c1[st][j], dv[st][j], hv[st][j]);
     };
 
     const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 acc[4][2];
+    f32x4 acc[2][2];
 #pragma unroll
-    for (int gi = 0; gi < 4; gi++) {
-        acc[gi][0] = zero4;
-        acc[gi][1] = zero4;
+    for (int h = 0; h < 2; h++) {
+        acc[h][0] = zero4;
+        acc[h][1] = zero4;
     }
 
     auto compute = [&](int st, int kk) {
@@ -129,18 +199,21 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
 #pragma unroll
         for (int bi = 0; bi < 4; bi++) {
             if (bi >= nb) break;
-            f16x8 wv[2];
+            f16x8 wv[2], wl[2];
             BlockScale bs[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 wv[j] = deq_block<DT>(c0[st][j], c1[st][j], hv[st][j], bi);
+                wl[j] = wv[j] * (_Float16)LO_INV_SCALE;
                 bs[j] = block_scale<DT>(dv[st][j], bi);
             }
 #pragma unroll
-            for (int gi = 0; gi < 4; gi++) {
-                const f16x8 xv = *(const f16x8 *)&sa[((bi * 4 + g) * 2 * GEMM_BM + 64 * wm + 16 * gi + cl) * 16];
+            for (int h = 0; h < 2; h++) {
+                const uint8_t *row = &sa[((bi * 4 + g) * 2 * GEMM_BM + 64 * wm + 32 * h + cl) * 16];
+                const f16x8 xh = *(const f16x8 *)row;
+                const f16x8 xl = *(const f16x8 *)(row + 16 * 16);
 #pragma unroll
-                for (int j = 0; j < 2; j++) mfma_block<DT>(acc[gi][j], xv, wv[j], bs[j]);
+                for (int j = 0; j < 2; j++) mfma_block_hl<DT>(acc[h][j], xh, xl, wv[j], wl[j], bs[j]);
             }
         }
     };
@@ -169,19 +242,19 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
     __syncthreads();
 
-    // lane l holds, per group gi and tile j, output row 16V + cl for vectors
-    // m0 + 32wm + 8gi + 2(l>>4) + {0, 1} (component pairs hi/lo)
+    // lane l holds, per vector group h and tile j, output row 16V + cl for
+    // vectors m0 + 32wm + 16h + 4(l>>4) + {0, 1, 2, 3}
 #pragma unroll
-    for (int gi = 0; gi < 4; gi++) {
+    for (int h = 0; h < 2; h++) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int V = nt_ * 8 + wn * 2 + j;
 #pragma unroll
-            for (int pr = 0; pr < 2; pr++) {
-                const int vi = 32 * wm + 8 * gi + 2 * (l >> 4) + pr;
+            for (int e = 0; e < 4; e++) {
+                const int vi = 32 * wm + 16 * h + 4 * (l >> 4) + e;
                 const int v = m0 + vi;
                 const bool act = v < n;
-                float y = (acc[gi][j][2 * pr] + acc[gi][j][2 * pr + 1] * LO_INV_SCALE) * ACT_INV_SCALE;
+                float y = acc[h][j][e] * ACT_INV_SCALE;
                 if (a.in.ss) y *= s_nrm[vi];
                 const int vv = act ? v : 0;
                 switch (sh.epi) {
@@ -211,6 +284,8 @@ int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
     sh.mts = (sh.mt + sh.ga - 1) / sh.ga;
     sh.nts = (sh.nt + 8 / sh.ga - 1) / (8 / sh.ga);
     const long wgs = 8L * sh.mts * sh.nts;
+    // the kernel's per-lane weight offsets are 32-bit
+    if ((size_t)a.w.row_tiles * a.w.block_quads * 64 * QFmt<DT>::LANE_BYTES > 0xffffffffUL) return -6;
     if (wgs > 0x7fffffffL) return -6;
     const size_t lds = (size_t)GEMM_STAGES * 4 * 4 * 2 * GEMM_BM * 16 + GEMM_BM * 4;
     if (a.ev_start)
