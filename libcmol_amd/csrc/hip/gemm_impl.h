@@ -3,9 +3,9 @@
 // format by gemm_q4.hip / gemm_q5.hip / gemm_q8.hip.
 //
 // One work-group computes a 64-vector x 128-row output tile.  Its eight waves
-// form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31 (A rows
-// 64wm.. of the hi/lo operand, four 16-row MFMA groups) and output rows
-// 32wn..32wn+31 (two 16-row "virtual tiles").  The k loop walks block quads
+// form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31 (two groups
+// of 16, each with a 16-row high and a 16-row low operand block in LDS) and
+// output rows 32wn..32wn+31 (two 16-row "virtual tiles").  The k loop walks block quads
 // through a two-stage pipeline: the activation operand of quad kk+1 is
 // copied into LDS with direct-to-LDS loads and each wave loads the weight
 // codes of its two virtual tiles for it into registers while quad kk is
@@ -15,9 +15,12 @@
 // for column c', the codes of row 16V + c' from tile (16V + c') / R,
 // column p*R + c' % R.
 //
-// Arithmetic is the decode matvec's (gemv_impl.h): codes decoded to exact
-// f16 integers, v_mfma_f32_16x16x32_f16 against the exact hi/lo operand,
-// fp32 per-block scaling, and the same fused epilogues.
+// Arithmetic follows the decode matvec's (gemv_impl.h): codes decoded to
+// exact f16 integers, v_mfma_f32_16x16x32_f16 against the exact hi/lo
+// operand, fp32 per-block scaling, and the same fused epilogues.  Unlike the
+// matvec, each block's low-part products join the high-part MFMA sum (codes
+// times 2^-11 against the low part times 2^11), so one scale FMA per output
+// and block serves both.
 #pragma once
 #include "gemv_impl.h"
 
