@@ -2,8 +2,9 @@
 // many activation vectors (n = prompt tokens), instantiated per weight
 // format by gemm_q4.hip / gemm_q5.hip / gemm_q8.hip.
 //
-// One work-group computes a 64-vector x 128-row output tile.  Its eight waves
-// form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31 (two groups
+// One work-group computes a 64-vector x 128-row output tile (32 x 128 with
+// four waves where 64-vector tiles would leave half the CUs idle).  Its eight
+// waves form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31 (two groups
 // of 16, each with a 16-row high and a 16-row low operand block in LDS) and
 // output rows 32wn..32wn+31 (two 16-row "virtual tiles").  The k loop walks block quads
 // through a two-stage pipeline: the activation operand of quad kk+1 is
@@ -24,10 +25,8 @@
 #pragma once
 #include "gemv_impl.h"
 
-#define GEMM_BM 64    // vectors per work-group
 #define GEMM_BN 128   // output rows per work-group (8 virtual tiles)
 #define GEMM_STAGES 2 // quads in flight
-#define GEMM_WAVES 8
 
 struct GemmShape {
     int epi;
@@ -99,13 +98,15 @@ __device__ __forceinline__ void gemm_wload(const QTensor &w, uint32_t e, uint32_
     else h = 0u;
 }
 
-template <int DT>
-__global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape sh)
+// WM wave rows of 32 vectors (GEMM_BM = 32 WM vectors per work-group, four
+// wave columns of 32 output rows: 4 WM waves)
+template <int DT, int WM>
+__global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
 {
-    constexpr int ASTAGE = 4 * 4 * 2 * GEMM_BM * 16;   // [block][k-group][128 rows][16 B]
+    constexpr int GEMM_BM = 32 * WM, GEMM_WAVES = 4 * WM;
+    constexpr int ASTAGE = 4 * 4 * 2 * GEMM_BM * 16;   // [block][k-group][2 GEMM_BM rows][16 B]
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *s_a = smem;                                 // GEMM_STAGES x ASTAGE
-    float *s_nrm = (float *)(smem + GEMM_STAGES * ASTAGE);
 
     // XCD-aware tile order: work-groups b, b+8, b+16, ... share an XCD.  The
     // (vector tile, row tile) grid is cut into ga x (8 / ga) slices, one per
@@ -119,14 +120,19 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, cl = l & 15;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid & 1, wn = wid >> 1;
+    const int wm = wid % WM, wn = wid / WM;
     const int n = a.n, nrows = 2 * n;
     const int BQ = a.w.block_quads, F = a.w.fold, R = 16 / F;
     const int nblk = a.w.cols >> 5;
     const int KQ = F * BQ;
 
-    // RMSNorm scales of the tile's vectors from the producer's partials
+    // RMSNorm scales of the tile's vectors from the producer's partials,
+    // passed through the last stage's LDS (untouched until the k loop's
+    // first copy into it, which follows a wait and a barrier) to the lanes
+    // that apply them: lane l's vectors 32wm + 16h + 4(l>>4) + e
+    float nrm[2][4] = {};
     if (a.in.ss) {
+        float *s_nrm = (float *)(smem + (GEMM_STAGES - 1) * ASTAGE);
         for (int vi = wid; vi < GEMM_BM; vi += GEMM_WAVES) {
             const int v = min(m0 + vi, n - 1);
             float s = 0.0f;
@@ -134,6 +140,11 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
             s = wave_sum(s);
             if (l == 0) s_nrm[vi] = 1.0f / sqrtf(s / (float)a.w.cols + a.in.eps);
         }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) nrm[h][e] = s_nrm[32 * wm + 16 * h + 4 * (l >> 4) + e];
     }
 
     // weight gather for this lane: virtual tile V -> (tile, column).  The
@@ -151,9 +162,9 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
     // operand rows of this lane's two 64-row halves (LDS rows of each 32-row
     // group: the 16 high parts, then the 16 low parts of its 16 vectors,
     // operand rows 2v and 2v+1)
-    uint32_t arow[2];
+    uint32_t arow[WM];
 #pragma unroll
-    for (int half = 0; half < 2; half++) {
+    for (int half = 0; half < WM; half++) {
         const int l5 = l & 31;
         arow[half] = 16u * (uint32_t)min(2 * m0 + 64 * half + (l & 32) + 2 * (l5 & 15) + (l5 >> 4), nrows - 1);
     }
@@ -171,8 +182,8 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
         const int b0 = p * 4 * BQ + 4 * q;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int s = wid * 4 + i;            // 16 (block, group) segments x 2 halves
-            const int seg = s >> 1, half = i & 1;
+            const int s = wid * 4 + i;            // 16 (block, group) segments x WM halves
+            const int seg = s / WM, half = i % WM;   // wid * 4 % WM == 0
             const int bi = seg >> 2, gg = seg & 3;
             const int blk = min(b0 + bi, nblk - 1);
             const uint8_t *src = (const uint8_t *)a.in.q + ((size_t)blk * 4 + gg) * nrows * 16 + arow[half];
@@ -241,7 +252,7 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
             compute(u, kk);
         }
     }
-    // drain the trailing re-reads before the LDS can be released; s_nrm visible
+    // drain the trailing re-reads before the LDS can be released
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
     __syncthreads();
 
@@ -258,7 +269,7 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
                 const int v = m0 + vi;
                 const bool act = v < n;
                 float y = acc[h][j][e] * ACT_INV_SCALE;
-                if (a.in.ss) y *= s_nrm[vi];
+                if (a.in.ss) y *= nrm[h][e];
                 const int vv = act ? v : 0;
                 switch (sh.epi) {
                 case EPI_STORE: epilogue<EPI_STORE>(a, V, cl, 16, vv, act, y); break;
@@ -271,30 +282,42 @@ __global__ __launch_bounds__(GEMM_WAVES * 64) void k_gemm(GemvArgs a, GemmShape 
     }
 }
 
-template <int DT>
-int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
+template <int DT, int WM>
+int launch_gemm_wm(const GemvArgs &a, int epi, hipStream_t s)
 {
-    if (epi < EPI_STORE || epi > EPI_QKV) return -6;
+    constexpr int BM = 32 * WM;
     GemmShape sh;
     sh.epi = epi;
-    sh.mt = (a.n + GEMM_BM - 1) / GEMM_BM;
+    sh.mt = (a.n + BM - 1) / BM;
     sh.vt = (a.w.rows + 15) / 16;
     sh.nt = (sh.vt + 7) / 8;
     // one slice of vector tiles per XCD (at M = 2048: 512 KiB of operand
-    // per vector tile, four per XCD) unless there are fewer vector tiles
+    // per 64-vector tile, four per XCD) unless there are fewer vector tiles
     sh.ga = 8;
     while (sh.ga > 1 && sh.ga > sh.mt) sh.ga >>= 1;
     sh.mts = (sh.mt + sh.ga - 1) / sh.ga;
     sh.nts = (sh.nt + 8 / sh.ga - 1) / (8 / sh.ga);
     const long wgs = 8L * sh.mts * sh.nts;
-    // the kernel's per-lane weight offsets are 32-bit
-    if ((size_t)a.w.row_tiles * a.w.block_quads * 64 * QFmt<DT>::LANE_BYTES > 0xffffffffUL) return -6;
     if (wgs > 0x7fffffffL) return -6;
-    const size_t lds = (size_t)GEMM_STAGES * 4 * 4 * 2 * GEMM_BM * 16 + GEMM_BM * 4;
+    const size_t lds = (size_t)GEMM_STAGES * 4 * 4 * 2 * BM * 16;
     if (a.ev_start)
-        hipExtLaunchKernelGGL(k_gemm<DT>, dim3((unsigned)wgs), dim3(GEMM_WAVES * 64), lds, s, a.ev_start,
+        hipExtLaunchKernelGGL((k_gemm<DT, WM>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a.ev_start,
                               a.ev_stop, 0, a, sh);
     else
-        hipLaunchKernelGGL(k_gemm<DT>, dim3((unsigned)wgs), dim3(GEMM_WAVES * 64), lds, s, a, sh);
+        hipLaunchKernelGGL((k_gemm<DT, WM>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a, sh);
     return 0;
+}
+
+// 64-vector work-groups (two per CU) unless their tiles cover at most half
+// the CUs (2048 output rows at 512 tokens: 128 tiles); then 32-vector ones
+// (five per CU), twice as many
+template <int DT>
+int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
+{
+    if (epi < EPI_STORE || epi > EPI_QKV) return -6;
+    // the kernel's per-lane weight offsets are 32-bit
+    if ((size_t)a.w.row_tiles * a.w.block_quads * 64 * QFmt<DT>::LANE_BYTES > 0xffffffffUL) return -6;
+    const long tiles64 = (long)((a.n + 63) / 64) * (((a.w.rows + 15) / 16 + 7) / 8);
+    if (tiles64 <= gemv_cus() / 2) return launch_gemm_wm<DT, 1>(a, epi, s);
+    return launch_gemm_wm<DT, 2>(a, epi, s);
 }
