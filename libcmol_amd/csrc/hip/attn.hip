@@ -300,14 +300,26 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 // ---------------------------------------------------------------------------
 // Prompt-pass attention over an fp32 cache, flash style on MFMA.
 //
-// The n vectors are consecutive prompt tokens of one session (vector v at
-// position seqlen[v] - 1).  One work-group of four waves per (kv head, block
-// of QT = 64 / G tokens, split of `split` positions): its QT x G query rows
-// (row r = token r / G, head r % G) share every K/V tile.  The work-group
-// walks its split's positions (up to its last token's) in tiles of 64:
-//   * the tile's K rows and V rows are read once and converted into f16 high
-//     and low parts in LDS (x = hi + lo / 2048), V transposed so that the
-//     weighted sum's B operand is contiguous;
+// k_kv_hilo first rewrites positions 0 .. last-1 of the session's layer cache
+// as exact f16 high and low parts (x = hi + lo / 2048) in the order the MFMA
+// operands are read: per (kv head, 32-position tile) one block of KVT_HALVES
+// halves,
+//   K: for column tile c (positions 16c..16c+15) and k-step s (dimensions
+//      32s..32s+31), a high and a low 1 KiB piece whose lane (col, g) holds
+//      dimensions 32s + 8g .. +7 of position 16c + col;
+//   V: for dimension tile t, a high and a low piece whose lane (col, g) holds
+//      positions 8g .. 8g+7 of dimension 16t + col (V transposed).
+// Positions past `last` repeat position last-1, so every value is finite.
+// Each prompt pass converts its cache prefix once per layer; before, every
+// work-group converted each tile it read (the prefix once per 64 query rows).
+//
+// k_attn_prompt: the n vectors are consecutive prompt tokens of one session
+// (vector v at position seqlen[v] - 1).  One work-group of four waves per (kv
+// head, block of QT = 64 / G tokens, split of `split` positions): its QT x G
+// query rows (row r = token r / G, head r % G) share every K/V tile.  The
+// work-group walks its split's positions (up to its last token's) in tiles of
+// 32, each copied whole into LDS with direct-to-LDS loads while the previous
+// tile is used:
 //   * wave w owns query rows 16w .. 16w+15; scores S = Q K^T come from three
 //     16x16x32 f16 MFMA products per step (hi.hi, hi.lo, lo.hi; the dropped
 //     lo.lo term is below 2^-22 of each product), scaled by 1/sqrt(d_head),
@@ -320,19 +332,68 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 // partial format of attn_split and k_attn_merge combines them.  Every
 // product is exact in fp32 and every sum fp32; the error against fp32
 // arithmetic is the dropped low-low term.
+constexpr int KVT_POS = 32;   // positions per tile
+
 template <int DH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_prompt(AttnArgs a)
+constexpr int kvt_halves() { return KVT_POS * DH * 4; }   // K and V, high and low
+
+template <int DH>
+__global__ __launch_bounds__(256) void k_kv_hilo(AttnArgs a, int last, _Float16 *hl, int tiles)
 {
 #pragma clang fp contract(off)
-    constexpr int TP = 32;              // positions per tile (LDS for two work-groups per CU)
-    constexpr int NDG = 256 / TP;       // staging threads per position
+    constexpr int KS = DH / 32, DT = DH / 16, TH = kvt_halves<DH>(), KH = TH / 2;
+    const int kvh = blockIdx.x, tile = blockIdx.y, tid = threadIdx.x;
+    const int p0 = tile * KVT_POS;
+    const size_t off = kv_offset(a.kv, 0) + (size_t)kvh * a.max_ctx * DH;
+    const float *kb = (const float *)a.kv.k_base + off;
+    const float *vb = (const float *)a.kv.v_base + off;
+    _Float16 *dst = hl + ((size_t)kvh * tiles + tile) * TH;
+    for (int it = tid; it < 2 * KS * 64; it += 256) {
+        const int lane = it & 63, cs = it >> 6, c = cs / KS, s = cs - c * KS;
+        const int p = min(p0 + 16 * c + (lane & 15), last - 1);
+        const float4 *src = (const float4 *)(kb + (size_t)p * DH + 32 * s + 8 * (lane >> 4));
+        const float4 x0 = src[0], x1 = src[1];
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        f16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            hi[e] = (_Float16)x[e];
+            lo[e] = (_Float16)((x[e] - (float)hi[e]) * 2048.0f);
+        }
+        *(f16x8 *)&dst[(cs * 2) * 512 + lane * 8] = hi;
+        *(f16x8 *)&dst[(cs * 2 + 1) * 512 + lane * 8] = lo;
+    }
+    for (int it = tid; it < DT * 64; it += 256) {
+        const int lane = it & 63, t = it >> 6, g = lane >> 4, col = lane & 15;
+        f16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int p = min(p0 + 8 * g + e, last - 1);
+            const float x = vb[(size_t)p * DH + 16 * t + col];
+            hi[e] = (_Float16)x;
+            lo[e] = (_Float16)((x - (float)hi[e]) * 2048.0f);
+        }
+        *(f16x8 *)&dst[KH + (t * 2) * 512 + lane * 8] = hi;
+        *(f16x8 *)&dst[KH + (t * 2 + 1) * 512 + lane * 8] = lo;
+    }
+}
+
+template <int DH>
+constexpr int attn_prompt_lds() { return 2 * kvt_halves<DH>() * 2 + 4 * 2 * 16 * KVT_POS * 2; }
+
+template <int DH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_prompt(AttnArgs a, const _Float16 *hl,
+                                                                                             int tiles)
+{
+#pragma clang fp contract(off)
+    constexpr int TP = KVT_POS;         // positions per tile
     constexpr int KS = DH / 32;         // MFMA k-steps over the head dimensions
     constexpr int DT = DH / 16;         // 16-dimension output tiles
-    constexpr int KR = DH + 8;          // K row stride in LDS (halves; rows 16-byte aligned)
-    constexpr int VS = TP + 8;          // transposed V row stride (halves)
-    __shared__ __attribute__((aligned(16))) _Float16 khi[TP * KR], klo[TP * KR];
-    __shared__ __attribute__((aligned(16))) _Float16 vhi[DH * VS], vlo[DH * VS];
-    __shared__ __attribute__((aligned(16))) _Float16 pw[4][2][16][TP];
+    constexpr int TH = kvt_halves<DH>(), KH = TH / 2;
+    constexpr int PIECES = TH * 2 / 1024 / 4;   // 1 KiB copies per wave and tile
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];
+    _Float16 *stg = lds_h;                                             // 2 x TH
+    _Float16(*pw)[2][16][TP] = (_Float16(*)[2][16][TP])(lds_h + 2 * TH);   // [wave][hi/lo][row][pos]
 
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, col = lane & 15;
     const int G = a.n_heads / a.n_kv, QT = 64 / G;
@@ -342,10 +403,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int last = min(a.seqlen[(size_t)(vb + nt - 1) * a.seqlen_stride], a.max_ctx);   // positions 0 .. last-1
     const int pa = sp * a.split, pb = min(pa + a.split, last);   // this split's positions
     if (pa >= last) return;
-    const size_t off = kv_offset(a.kv, vb) + (size_t)kvh * a.max_ctx * DH;
-    const float *kb = (const float *)a.kv.k_base + off;
-    const float *vbp = (const float *)a.kv.v_base + off;
     const float scale = 1.0f / sqrtf((float)DH);
+    const uint8_t *tsrc = (const uint8_t *)(hl + ((size_t)kvh * tiles + pa / TP) * TH);
+    // tile j of the split into stage st: 4 x PIECES pieces of 1 KiB
+    auto issue = [&](int st, int j) {
+        const uint8_t *src = tsrc + (size_t)j * TH * 2;
+        uint8_t *dst = (uint8_t *)(stg + st * TH);
+#pragma unroll
+        for (int i = 0; i < PIECES; i++) {
+            const int pc = wid * PIECES + i;
+            __builtin_amdgcn_global_load_lds((const gvoid_t *)(src + pc * 1024 + lane * 16),
+                                             (lvoid_t *)(dst + pc * 1024), 16, 0, 0);
+        }
+    };
+    const int ntiles = (pb - pa + TP - 1) / TP;
+    issue(0, 0);
 
     // A operand: lane feeds row 16w + col (token, head) with dimensions
     // 32s + 8g .. +7 of k-step s, high and low parts
@@ -388,32 +460,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         o2[t] = zero4;
     }
 
-    const int ntiles = (pb - pa + TP - 1) / TP;
     for (int j = 0; j < ntiles; j++) {
         const int p0 = pa + j * TP;
-        // ---- stage K (row-major) and V (transposed) of positions p0 ..
-        // p0+TP-1: thread = (position tid % TP, dimension quads tid / TP +
-        // NDG k) ----
-        {
-            const int pl = tid % TP, dg = tid / TP;
-            const int p = min(p0 + pl, pb - 1);
-            const float *kr = kb + (size_t)p * DH, *vr = vbp + (size_t)p * DH;
-#pragma unroll 4
-            for (int d4 = dg; d4 < DH / 4; d4 += NDG) {
-                const float4 kx = *(const float4 *)(kr + 4 * d4);
-                const float4 vx = *(const float4 *)(vr + 4 * d4);
-                const float kv[4] = {kx.x, kx.y, kx.z, kx.w}, vv[4] = {vx.x, vx.y, vx.z, vx.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const _Float16 kh = (_Float16)kv[e], vh = (_Float16)vv[e];
-                    khi[pl * KR + 4 * d4 + e] = kh;
-                    klo[pl * KR + 4 * d4 + e] = (_Float16)((kv[e] - (float)kh) * 2048.0f);
-                    vhi[(4 * d4 + e) * VS + pl] = vh;
-                    vlo[(4 * d4 + e) * VS + pl] = (_Float16)((vv[e] - (float)vh) * 2048.0f);
-                }
-            }
-        }
+        // tile j is in stage j & 1 once this wave's copies have landed and
+        // every wave has passed the barrier (which also means every wave is
+        // done with tile j - 1, whose stage the copy of tile j + 1 reuses)
+        __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
         __syncthreads();
+        if (j + 1 < ntiles) issue((j + 1) & 1, j + 1);
+        const _Float16 *ks_ = stg + (j & 1) * TH, *vs_ = ks_ + KH;
         // ---- scores of the tile's positions (16-position column tiles) ----
         constexpr int NC = TP / 16;
         float sc[NC][4];   // [column tile][row i]
@@ -423,8 +478,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             const int kp = 16 * c + col;
 #pragma unroll
             for (int s = 0; s < KS; s++) {
-                const f16x8 bh = *(const f16x8 *)&khi[kp * KR + 32 * s + 8 * g];
-                const f16x8 bl = *(const f16x8 *)&klo[kp * KR + 32 * s + 8 * g];
+                const f16x8 bh = *(const f16x8 *)&ks_[((c * KS + s) * 2) * 512 + lane * 8];
+                const f16x8 bl = *(const f16x8 *)&ks_[((c * KS + s) * 2 + 1) * 512 + lane * 8];
                 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], bh, s1, 0, 0, 0);
                 s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], bl, s2, 0, 0, 0);
                 s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s], bh, s2, 0, 0, 0);
@@ -480,20 +535,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
         __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int ks = 0; ks < TP / 32; ks++) {
-            const f16x8 ph = *(const f16x8 *)&pw[wid][0][col][32 * ks + 8 * g];
-            const f16x8 pl = *(const f16x8 *)&pw[wid][1][col][32 * ks + 8 * g];
+        {
+            const f16x8 ph = *(const f16x8 *)&pw[wid][0][col][8 * g];
+            const f16x8 pl = *(const f16x8 *)&pw[wid][1][col][8 * g];
 #pragma unroll
             for (int t = 0; t < DT; t++) {
-                const f16x8 bh = *(const f16x8 *)&vhi[(16 * t + col) * VS + 32 * ks + 8 * g];
-                const f16x8 bl = *(const f16x8 *)&vlo[(16 * t + col) * VS + 32 * ks + 8 * g];
+                const f16x8 bh = *(const f16x8 *)&vs_[(t * 2) * 512 + lane * 8];
+                const f16x8 bl = *(const f16x8 *)&vs_[(t * 2 + 1) * 512 + lane * 8];
                 o1[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bh, o1[t], 0, 0, 0);
                 o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bl, o2[t], 0, 0, 0);
                 o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bh, o2[t], 0, 0, 0);
             }
         }
-        __syncthreads();   // K / V / P areas are rewritten by the next tile
+        __builtin_amdgcn_wave_barrier();   // this wave's P rows are rewritten by the next tile
     }
 
     // ---- outputs: lane holds rows 16w + 4g + i, dimension 16t + col ----
@@ -524,20 +578,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
 }
 
-int launch_attn_prompt(const AttnArgs &a, hipStream_t s)
+size_t attn_prompt_kv_bytes(int n_kv, int d_head, int max_ctx)
+{
+    const size_t tiles = (size_t)(max_ctx + KVT_POS - 1) / KVT_POS;
+    return (size_t)n_kv * tiles * KVT_POS * d_head * 4 * sizeof(_Float16);
+}
+
+template <int DH>
+int launch_attn_prompt_dh(const AttnArgs &a, _Float16 *kv_hl, int last, hipStream_t s)
+{
+    static const bool lds_ok =
+        hipFuncSetAttribute((const void *)k_attn_prompt<DH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            attn_prompt_lds<DH>()) == hipSuccess;
+    if (!lds_ok) return -4;
+    const int G = a.n_heads / a.n_kv, QT = 64 / G;
+    const int tiles = (a.max_ctx + KVT_POS - 1) / KVT_POS;
+    hipLaunchKernelGGL(k_kv_hilo<DH>, dim3(a.n_kv, (last + KVT_POS - 1) / KVT_POS), dim3(256), 0, s, a, last,
+                       kv_hl, tiles);
+    const dim3 grid(a.n_kv, (a.n + QT - 1) / QT, a.max_splits), block(256), mgrid(a.n_heads, a.n);
+    hipLaunchKernelGGL(k_attn_prompt<DH>, grid, block, attn_prompt_lds<DH>(), s, a, kv_hl, tiles);
+    if (a.max_splits > 1) hipLaunchKernelGGL((k_attn_merge<DH>), mgrid, block, 0, s, a);
+    return 0;
+}
+
+int launch_attn_prompt(const AttnArgs &a, _Float16 *kv_hl, int last, hipStream_t s)
 {
     const int G = a.n_heads / a.n_kv;
     if (a.kv_f16 || G < 1 || G > 8 || a.n_heads % a.n_kv || a.n < 1 || (a.d_head != 64 && a.d_head != 128))
         return -4;
-    if (a.split < 64 || a.max_splits > ATT_MAX_MERGE) return -4;
-    const int QT = 64 / G;
-    const dim3 grid(a.n_kv, (a.n + QT - 1) / QT, a.max_splits), block(256), mgrid(a.n_heads, a.n);
-    if (a.d_head == 128) hipLaunchKernelGGL(k_attn_prompt<128>, grid, block, 0, s, a);
-    else hipLaunchKernelGGL(k_attn_prompt<64>, grid, block, 0, s, a);
-    if (a.max_splits > 1) {
-        if (a.d_head == 128) hipLaunchKernelGGL((k_attn_merge<128>), mgrid, block, 0, s, a);
-        else hipLaunchKernelGGL((k_attn_merge<64>), mgrid, block, 0, s, a);
-    }
+    if (a.split < 64 || a.split % KVT_POS || a.max_splits > ATT_MAX_MERGE) return -4;
+    if (!kv_hl || last < 1 || last > a.max_ctx) return -4;
+    const int rc = a.d_head == 128 ? launch_attn_prompt_dh<128>(a, kv_hl, last, s)
+                                   : launch_attn_prompt_dh<64>(a, kv_hl, last, s);
+    if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

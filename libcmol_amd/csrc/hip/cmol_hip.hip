@@ -558,6 +558,7 @@ struct Prefill {
     float *ss_a = nullptr, *ss_b = nullptr;   // [cap][d]
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
     float *qkv_raw = nullptr;                 // QK-norm models: [cap][d + 2 kvd]
+    _Float16 *kv_hl = nullptr;                // prompt attention: high/low f16 copy of one layer's cache
     int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
     std::mutex mu;
@@ -915,6 +916,7 @@ void plan_prefill(Plan &P, const cmolhip_model_desc_t *d)
     P.add((size_t)cap * np * 4);
     P.add((size_t)cap * np * h.d_head * 4);
     if (has_qk_norm(d)) P.add((size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head) * 4);
+    if (prompt_attn_fits(h)) P.add(attn_prompt_kv_bytes(h.n_kv_heads, h.d_head, h.max_ctx));
 }
 
 
@@ -1297,7 +1299,7 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         at.next = act_out(F.op_o, L.o.dtype, n, nullptr, nullptr, 0);
         // the pass's tokens share every K/V tile (flash style on MFMA); other
         // shapes and fp16 caches take the split kernels
-        if (prompt_attn_on() && launch_attn_prompt(at, st) == 0) {
+        if (prompt_attn_on() && launch_attn_prompt(at, F.kv_hl, F.h_steps[3 * (n - 1) + 2], st) == 0) {
         } else {
             RC(launch_attn(at, st));
         }
@@ -1421,6 +1423,8 @@ int build_prefill(cmolhip_model *m, Prefill &F)
     RC(arena_get(c, (size_t)cap * np, &F.pl));
     RC(arena_get(c, (size_t)cap * np * h.d_head, &F.po));
     if (m->qk_norm) RC(arena_get(c, (size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head), &F.qkv_raw));
+    if (prompt_attn_fits(h))
+        RC(arena_get(c, attn_prompt_kv_bytes(h.n_kv_heads, h.d_head, h.max_ctx) / sizeof(_Float16), &F.kv_hl));
     HC(hipHostMalloc((void **)&F.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
     HC(hipHostMalloc((void **)&F.h_slots, (size_t)cap * 4, hipHostMallocDefault));
     return E_OK;

@@ -22,13 +22,6 @@ struct GemvShape {
     int ss_bytes;   // LDS bytes of the sum-of-squares partials
 };
 
-typedef __attribute__((address_space(1))) void gvoid_t;
-typedef __attribute__((address_space(3))) void lvoid_t;
-
-// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
-// expcnt 6:4, lgkmcnt 11:8)
-#define WAITCNT_VM_LGKM0(N) (((N) & 15) | (((N) >> 4) << 14) | (7 << 4))
-
 template <typename M = StPlain>
 __device__ inline void store_kv(void *base, int kv_f16, size_t idx, float v)
 {

@@ -277,7 +277,10 @@ int launch_attn(const AttnArgs &a, hipStream_t s);
 // Prompt-pass attention (flash style on MFMA) for vectors that are
 // consecutive tokens of one session over an fp32 cache, d_head 64 / 128;
 // returns -4 for shapes it does not take (the caller runs launch_attn).
-int launch_attn_prompt(const AttnArgs &a, hipStream_t s);
+// kv_hl: attn_prompt_kv_bytes of scratch for the high/low f16 copy of the
+// session's cache positions 0 .. last-1 (last = the pass's largest seqlen).
+int launch_attn_prompt(const AttnArgs &a, _Float16 *kv_hl, int last, hipStream_t s);
+size_t attn_prompt_kv_bytes(int n_kv, int d_head, int max_ctx);
 
 // QK-norm models (src/attn.c:62-101): the QKV matvec stores raw q|k|v rows;
 // this stage normalises each q and k head (RMSNorm over d_head, weights
