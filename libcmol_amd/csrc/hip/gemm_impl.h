@@ -98,12 +98,14 @@ __device__ __forceinline__ void gemm_wload(const QTensor &w, uint32_t e, uint32_
     else h = 0u;
 }
 
-// WM wave rows of 32 vectors (GEMM_BM = 32 WM vectors per work-group, four
-// wave columns of 32 output rows: 4 WM waves)
-template <int DT, int WM>
+// WM wave rows of HG groups of 16 vectors each (GEMM_BM = 16 HG WM vectors
+// per work-group), four wave columns of 32 output rows: 4 WM waves
+template <int DT, int WM, int HG>
 __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
 {
-    constexpr int GEMM_BM = 32 * WM, GEMM_WAVES = 4 * WM;
+    constexpr int GEMM_BM = 16 * HG * WM, GEMM_WAVES = 4 * WM;
+    constexpr int SEGS = GEMM_BM / 32;            // 64-row operand segments per (block, group)
+    constexpr int PW = 16 * SEGS / GEMM_WAVES;    // operand copies per wave and stage
     constexpr int ASTAGE = 4 * 4 * 2 * GEMM_BM * 16;   // [block][k-group][2 GEMM_BM rows][16 B]
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *s_a = smem;                                 // GEMM_STAGES x ASTAGE
@@ -129,8 +131,8 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     // RMSNorm scales of the tile's vectors from the producer's partials,
     // passed through the last stage's LDS (untouched until the k loop's
     // first copy into it, which follows a wait and a barrier) to the lanes
-    // that apply them: lane l's vectors 32wm + 16h + 4(l>>4) + e
-    float nrm[2][4] = {};
+    // that apply them: lane l's vectors 16 HG wm + 16h + 4(l>>4) + e
+    float nrm[HG][4] = {};
     if (a.in.ss) {
         float *s_nrm = (float *)(smem + (GEMM_STAGES - 1) * ASTAGE);
         for (int vi = wid; vi < GEMM_BM; vi += GEMM_WAVES) {
@@ -142,9 +144,9 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
         }
         __syncthreads();
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+        for (int h = 0; h < HG; h++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) nrm[h][e] = s_nrm[32 * wm + 16 * h + 4 * (l >> 4) + e];
+            for (int e = 0; e < 4; e++) nrm[h][e] = s_nrm[16 * HG * wm + 16 * h + 4 * (l >> 4) + e];
     }
 
     // weight gather for this lane: virtual tile V -> (tile, column).  The
@@ -162,9 +164,9 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     // operand rows of this lane's two 64-row halves (LDS rows of each 32-row
     // group: the 16 high parts, then the 16 low parts of its 16 vectors,
     // operand rows 2v and 2v+1)
-    uint32_t arow[WM];
+    uint32_t arow[SEGS];
 #pragma unroll
-    for (int half = 0; half < WM; half++) {
+    for (int half = 0; half < SEGS; half++) {
         const int l5 = l & 31;
         arow[half] = 16u * (uint32_t)min(2 * m0 + 64 * half + (l & 32) + 2 * (l5 & 15) + (l5 >> 4), nrows - 1);
     }
@@ -181,9 +183,9 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
         const int p = kk / BQ, q = kk - p * BQ;
         const int b0 = p * 4 * BQ + 4 * q;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int s = wid * 4 + i;            // 16 (block, group) segments x WM halves
-            const int seg = s / WM, half = i % WM;   // wid * 4 % WM == 0
+        for (int i = 0; i < PW; i++) {
+            const int s = wid * PW + i;           // 16 (block, group) pairs x SEGS segments
+            const int seg = s / SEGS, half = i % SEGS;   // wid * PW % SEGS == 0
             const int bi = seg >> 2, gg = seg & 3;
             const int blk = min(b0 + bi, nblk - 1);
             const uint8_t *src = (const uint8_t *)a.in.q + ((size_t)blk * 4 + gg) * nrows * 16 + arow[half];
@@ -197,9 +199,9 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     };
 
     const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 acc[2][2];
+    f32x4 acc[HG][2];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < HG; h++) {
         acc[h][0] = zero4;
         acc[h][1] = zero4;
     }
@@ -222,8 +224,8 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
                 bs[j] = block_scale<DT>(dv[st][j], bi);
             }
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint8_t *row = &sa[((bi * 4 + g) * 2 * GEMM_BM + 64 * wm + 32 * h + cl) * 16];
+            for (int h = 0; h < HG; h++) {
+                const uint8_t *row = &sa[((bi * 4 + g) * 2 * GEMM_BM + 32 * HG * wm + 32 * h + cl) * 16];
                 const f16x8 xh = *(const f16x8 *)row;
                 const f16x8 xl = *(const f16x8 *)(row + 16 * 16);
 #pragma unroll
@@ -257,15 +259,15 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     __syncthreads();
 
     // lane l holds, per vector group h and tile j, output row 16V + cl for
-    // vectors m0 + 32wm + 16h + 4(l>>4) + {0, 1, 2, 3}
+    // vectors m0 + 16 HG wm + 16h + 4(l>>4) + {0, 1, 2, 3}
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < HG; h++) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int V = nt_ * 8 + wn * 2 + j;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int vi = 32 * wm + 16 * h + 4 * (l >> 4) + e;
+                const int vi = 16 * HG * wm + 16 * h + 4 * (l >> 4) + e;
                 const int v = m0 + vi;
                 const bool act = v < n;
                 float y = acc[h][j][e] * ACT_INV_SCALE;
@@ -282,10 +284,10 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     }
 }
 
-template <int DT, int WM>
+template <int DT, int WM, int HG>
 int launch_gemm_wm(const GemvArgs &a, int epi, hipStream_t s)
 {
-    constexpr int BM = 32 * WM;
+    constexpr int BM = 16 * HG * WM;
     GemmShape sh;
     sh.epi = epi;
     sh.mt = (a.n + BM - 1) / BM;
@@ -301,16 +303,20 @@ int launch_gemm_wm(const GemvArgs &a, int epi, hipStream_t s)
     if (wgs > 0x7fffffffL) return -6;
     const size_t lds = (size_t)GEMM_STAGES * 4 * 4 * 2 * BM * 16;
     if (a.ev_start)
-        hipExtLaunchKernelGGL((k_gemm<DT, WM>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a.ev_start,
+        hipExtLaunchKernelGGL((k_gemm<DT, WM, HG>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a.ev_start,
                               a.ev_stop, 0, a, sh);
     else
-        hipLaunchKernelGGL((k_gemm<DT, WM>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a, sh);
+        hipLaunchKernelGGL((k_gemm<DT, WM, HG>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a, sh);
     return 0;
 }
 
 // 64-vector work-groups (two per CU) unless their tiles cover at most half
 // the CUs (2048 output rows at 512 tokens: 128 tiles); then 32-vector ones
-// (five per CU), twice as many
+// (five per CU), twice as many.  Four-wave 64-vector work-groups (four
+// vector groups per wave: fewer decode and address instructions per
+// product, 140 VGPRs, two waves per SIMD) ran 10-15 % slower at 2048 tokens:
+// the kernel needs the waves to hide latency more than it needs fewer
+// instructions.
 template <int DT>
 int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
 {
@@ -318,6 +324,6 @@ int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
     // the kernel's per-lane weight offsets are 32-bit
     if ((size_t)a.w.row_tiles * a.w.block_quads * 64 * QFmt<DT>::LANE_BYTES > 0xffffffffUL) return -6;
     const long tiles64 = (long)((a.n + 63) / 64) * (((a.w.rows + 15) / 16 + 7) / 8);
-    if (tiles64 <= gemv_cus() / 2) return launch_gemm_wm<DT, 1>(a, epi, s);
-    return launch_gemm_wm<DT, 2>(a, epi, s);
+    if (tiles64 <= gemv_cus() / 2) return launch_gemm_wm<DT, 1, 2>(a, epi, s);
+    return launch_gemm_wm<DT, 2, 2>(a, epi, s);
 }
