@@ -212,9 +212,7 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
         // past the end of the k range contribute nothing
         const int nb = kk < KQ ? min(4, nblk - (p * 4 * BQ + 4 * q)) : 0;
         const uint8_t *sa = s_a + st * ASTAGE;
-#pragma unroll
-        for (int bi = 0; bi < 4; bi++) {
-            if (bi >= nb) break;
+        auto block = [&](int bi) {
             f16x8 wv[2], wl[2];
             BlockScale bs[2];
 #pragma unroll
@@ -230,6 +228,19 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
                 const f16x8 xl = *(const f16x8 *)(row + 16 * 16);
 #pragma unroll
                 for (int j = 0; j < 2; j++) mfma_block_hl<DT>(acc[h][j], xh, xl, wv[j], wl[j], bs[j]);
+            }
+        };
+        // a whole quad is one straight run (the four blocks' loads, MFMA
+        // chains and scale FMAs interleave); the uniform test keeps branches
+        // between blocks to the rare partial quads
+        if (nb == 4) {
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++) block(bi);
+        } else {
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++) {
+                if (bi >= nb) break;
+                block(bi);
             }
         }
     };
