@@ -308,7 +308,8 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 //      32s..32s+31), a high and a low 1 KiB piece whose lane (col, g) holds
 //      dimensions 32s + 8g .. +7 of position 16c + col;
 //   V: for dimension tile t, a high and a low piece whose lane (col, g) holds
-//      positions 8g .. 8g+7 of dimension 16t + col (V transposed).
+//      dimension 16t + col of positions 4g .. 4g+3 and 16+4g .. 16+4g+3 (the
+//      positions whose scores that lane holds after the score products).
 // Positions past `last` repeat position last-1, so every value is finite.
 // Each prompt pass converts its cache prefix once per layer; before, every
 // work-group converted each tile it read (the prefix once per 64 query rows).
@@ -319,14 +320,16 @@ int launch_qk_rope(const QkArgs &a, hipStream_t s)
 // query rows (row r = token r / G, head r % G) share every K/V tile.  The
 // work-group walks its split's positions (up to its last token's) in tiles of
 // 32, each copied whole into LDS with direct-to-LDS loads while the previous
-// tile is used:
-//   * wave w owns query rows 16w .. 16w+15; scores S = Q K^T come from three
-//     16x16x32 f16 MFMA products per step (hi.hi, hi.lo, lo.hi; the dropped
-//     lo.lo term is below 2^-22 of each product), scaled by 1/sqrt(d_head),
-//     positions past a row's token masked (causal);
-//   * online softmax per row (max and sum over the 16-lane groups that hold
-//     the row), the weights written to LDS as f16 high / low parts;
-//   * O += P V with the same three products per step.
+// tile is used.  Wave w owns query rows 16w .. 16w+15, lane (col, g) row
+// 16w + col:
+//   * transposed scores S^T = K Q^T from three 16x16x32 f16 MFMA products per
+//     step (hi.hi, lo.hi, hi.lo; the dropped lo.lo term is below 2^-22 of
+//     each product), scaled by 1/sqrt(d_head), positions past a row's token
+//     masked (causal): lane (col, g) holds positions 16c + 4g + i of its row;
+//   * online softmax per row over the row's four lanes (two butterfly steps);
+//   * the weights, split into f16 high / low parts in registers, are the B
+//     operand of O^T = V^T P^T (same three products), whose k order is the
+//     V pieces' position order: no weight goes through LDS.
 // A token whose positions fit one split is finished here (out / next);
 // otherwise each split leaves (max, sum of exp, unnormalised output) in the
 // partial format of attn_split and k_attn_merge combines them.  Every
@@ -368,7 +371,7 @@ __global__ __launch_bounds__(256) void k_kv_hilo(AttnArgs a, int last, _Float16 
         f16x8 hi, lo;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const int p = min(p0 + 8 * g + e, last - 1);
+            const int p = min(p0 + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4), last - 1);
             const float x = vb[(size_t)p * DH + 16 * t + col];
             hi[e] = (_Float16)x;
             lo[e] = (_Float16)((x - (float)hi[e]) * 2048.0f);
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(256) void k_kv_hilo(AttnArgs a, int last, _Float16 
 }
 
 template <int DH>
-constexpr int attn_prompt_lds() { return 2 * kvt_halves<DH>() * 2 + 4 * 2 * 16 * KVT_POS * 2; }
+constexpr int attn_prompt_lds() { return 2 * kvt_halves<DH>() * 2; }
 
 template <int DH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_prompt(AttnArgs a, const _Float16 *hl,
@@ -392,8 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     constexpr int TH = kvt_halves<DH>(), KH = TH / 2;
     constexpr int PIECES = TH * 2 / 1024 / 4;   // 1 KiB copies per wave and tile
     extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];
-    _Float16 *stg = lds_h;                                             // 2 x TH
-    _Float16(*pw)[2][16][TP] = (_Float16(*)[2][16][TP])(lds_h + 2 * TH);   // [wave][hi/lo][row][pos]
+    _Float16 *stg = lds_h;                      // 2 x TH
 
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, g = lane >> 4, col = lane & 15;
     const int G = a.n_heads / a.n_kv, QT = 64 / G;
@@ -419,8 +421,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int ntiles = (pb - pa + TP - 1) / TP;
     issue(0, 0);
 
-    // A operand: lane feeds row 16w + col (token, head) with dimensions
-    // 32s + 8g .. +7 of k-step s, high and low parts
+    // this lane's query row 16w + col = (token at, head ah); its B operand of
+    // the scores: dimensions 32s + 8g .. +7 of k-step s, high and low parts
     const int ar = 16 * wid + col, at = ar / G, ah = ar - at * G;
     const bool arow = at < nt;
     f16x8 qh[KS], ql[KS];
@@ -437,21 +439,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
     }
-    // C rows of this lane: 16w + 4g + i, i = 0..3 -> (token, position limit)
-    int lim[4], nact[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 16 * wid + 4 * g + i, t = r / G;
-        const int L = t < nt ? min(a.seqlen[(size_t)(vb + t) * a.seqlen_stride], a.max_ctx) : 0;
-        nact[i] = (L + a.split - 1) / a.split;
-        lim[i] = min(L, pb);   // visible positions of this split: pa .. lim-1
-    }
-    float m[4], lsum[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        m[i] = -INFINITY;
-        lsum[i] = 0.0f;
-    }
+    const int L = arow ? min(a.seqlen[(size_t)(vb + at) * a.seqlen_stride], a.max_ctx) : 0;
+    const int nact = (L + a.split - 1) / a.split;
+    const int lim = min(L, pb);   // visible positions of this split: pa .. lim-1
+    float m = -INFINITY, lsum = 0.0f;
     const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 o1[DT], o2[DT];
 #pragma unroll
@@ -469,111 +460,103 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         __syncthreads();
         if (j + 1 < ntiles) issue((j + 1) & 1, j + 1);
         const _Float16 *ks_ = stg + (j & 1) * TH, *vs_ = ks_ + KH;
-        // ---- scores of the tile's positions (16-position column tiles) ----
-        constexpr int NC = TP / 16;
-        float sc[NC][4];   // [column tile][row i]
+        // ---- transposed scores: sc[c][i] = position 16c + 4g + i ----
+        float sc[2][4];
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
+        for (int c = 0; c < 2; c++) {
             f32x4 s1 = zero4, s2 = zero4;
-            const int kp = 16 * c + col;
 #pragma unroll
             for (int s = 0; s < KS; s++) {
-                const f16x8 bh = *(const f16x8 *)&ks_[((c * KS + s) * 2) * 512 + lane * 8];
-                const f16x8 bl = *(const f16x8 *)&ks_[((c * KS + s) * 2 + 1) * 512 + lane * 8];
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], bh, s1, 0, 0, 0);
-                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], bl, s2, 0, 0, 0);
-                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s], bh, s2, 0, 0, 0);
+                const f16x8 kh = *(const f16x8 *)&ks_[((c * KS + s) * 2) * 512 + lane * 8];
+                const f16x8 kl = *(const f16x8 *)&ks_[((c * KS + s) * 2 + 1) * 512 + lane * 8];
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], s1, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], s2, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], s2, 0, 0, 0);
             }
-            const int pos = p0 + kp;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                sc[c][i] = pos < lim[i] ? (s1[i] + s2[i] * (1.0f / 2048.0f)) * scale : -INFINITY;
-        }
-        // ---- online softmax per row: the row's scores are in the 16 lanes
-        // of group g, NC per lane ----
-        float alpha[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float mx = sc[0][i];
-#pragma unroll
-            for (int c = 1; c < NC; c++) mx = fmaxf(mx, sc[c][i]);
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-            const float mn = fmaxf(m[i], mx);
-            // a row with no visible position yet keeps m = -inf: weights 0
-            const float mref = mn == -INFINITY ? 0.0f : mn;
-            alpha[i] = expf(m[i] - mref);
-            float ps = 0.0f;
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const float e = expf(sc[c][i] - mref);
-                sc[c][i] = e;
-                ps += e;
-            }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) ps += __shfl_xor(ps, o, 64);
-            lsum[i] = lsum[i] * alpha[i] + ps;
-            m[i] = mn;
-        }
-        // weights to this wave's LDS rows: P[row 4g+i][position 16c+col]
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const _Float16 eh = (_Float16)sc[c][i];
-                pw[wid][0][4 * g + i][16 * c + col] = eh;
-                pw[wid][1][4 * g + i][16 * c + col] = (_Float16)((sc[c][i] - (float)eh) * 2048.0f);
+                const int pos = p0 + 16 * c + 4 * g + i;
+                sc[c][i] = pos < lim ? (s1[i] + s2[i] * (1.0f / 2048.0f)) * scale : -INFINITY;
             }
         }
-        // ---- O = alpha O + P V ----
+        // ---- online softmax of the row: its 32 scores are in lanes col,
+        // col + 16, col + 32, col + 48 ----
+        float mx = sc[0][0];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[c][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);
+        // a row with no visible position yet keeps m = -inf: weights 0
+        const float mref = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = expf(m - mref);
+        float ps = 0.0f;
+        f16x8 ph, pl;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = expf(sc[c][i] - mref);
+                ps += e;
+                const _Float16 eh = (_Float16)e;
+                ph[4 * c + i] = eh;
+                pl[4 * c + i] = (_Float16)((e - (float)eh) * 2048.0f);
+            }
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        lsum = lsum * alpha + ps;
+        m = mn;
+        // ---- O^T = alpha O^T + V^T P^T ----
 #pragma unroll
         for (int t = 0; t < DT; t++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                o1[t][i] *= alpha[i];
-                o2[t][i] *= alpha[i];
+                o1[t][i] *= alpha;
+                o2[t][i] *= alpha;
             }
         }
-        __builtin_amdgcn_wave_barrier();
-        {
-            const f16x8 ph = *(const f16x8 *)&pw[wid][0][col][8 * g];
-            const f16x8 pl = *(const f16x8 *)&pw[wid][1][col][8 * g];
 #pragma unroll
-            for (int t = 0; t < DT; t++) {
-                const f16x8 bh = *(const f16x8 *)&vs_[(t * 2) * 512 + lane * 8];
-                const f16x8 bl = *(const f16x8 *)&vs_[(t * 2 + 1) * 512 + lane * 8];
-                o1[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bh, o1[t], 0, 0, 0);
-                o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bl, o2[t], 0, 0, 0);
-                o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bh, o2[t], 0, 0, 0);
-            }
+        for (int t = 0; t < DT; t++) {
+            const f16x8 vh = *(const f16x8 *)&vs_[(t * 2) * 512 + lane * 8];
+            const f16x8 vl = *(const f16x8 *)&vs_[(t * 2 + 1) * 512 + lane * 8];
+            o1[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, o1[t], 0, 0, 0);
+            o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, o2[t], 0, 0, 0);
+            o2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, o2[t], 0, 0, 0);
         }
-        __builtin_amdgcn_wave_barrier();   // this wave's P rows are rewritten by the next tile
     }
 
-    // ---- outputs: lane holds rows 16w + 4g + i, dimension 16t + col ----
+    // ---- outputs: lane (col, g) holds dimensions 16t + 4g + i of its row ----
+    if (!arow || sp >= nact) return;   // no positions of this token here
+    const int v = vb + at;
+    if (nact == 1) {
+        const float inv = 1.0f / lsum;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 16 * wid + 4 * g + i, t = r / G, h = r - t * G;
-        if (t >= nt || sp >= nact[i]) continue;   // no positions of this token here
-        const int v = vb + t;
-        if (nact[i] == 1) {
-            const float inv = 1.0f / lsum[i];
+        for (int t = 0; t < DT; t++) {
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const float ov = (o1[dt][i] + o2[dt][i] * (1.0f / 2048.0f)) * inv;
-                const int k = (kvh * G + h) * DH + 16 * dt + col;
+            for (int i = 0; i < 4; i++) {
+                const float ov = (o1[t][i] + o2[t][i] * (1.0f / 2048.0f)) * inv;
+                const int k = (kvh * G + ah) * DH + 16 * t + 4 * g + i;
                 if (a.out) a.out[(size_t)v * a.out_stride + k] = ov;
                 if (a.next.q) act_put(a.next, v, k, ov);
             }
-        } else {
-            const size_t sb = (((size_t)v * a.n_kv + kvh) * a.max_splits + sp) * G + h;
+        }
+    } else {
+        const size_t sb = (((size_t)v * a.n_kv + kvh) * a.max_splits + sp) * G + ah;
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-                a.po[sb * DH + 16 * dt + col] = o1[dt][i] + o2[dt][i] * (1.0f / 2048.0f);
-            if (col == 0) {
-                a.pm[sb] = m[i];
-                a.pl[sb] = lsum[i];
-            }
+        for (int t = 0; t < DT; t++) {
+            float4 ov;
+            ov.x = o1[t][0] + o2[t][0] * (1.0f / 2048.0f);
+            ov.y = o1[t][1] + o2[t][1] * (1.0f / 2048.0f);
+            ov.z = o1[t][2] + o2[t][2] * (1.0f / 2048.0f);
+            ov.w = o1[t][3] + o2[t][3] * (1.0f / 2048.0f);
+            *(float4 *)&a.po[sb * DH + 16 * t + 4 * g] = ov;
+        }
+        if (g == 0) {
+            a.pm[sb] = m;
+            a.pl[sb] = lsum;
         }
     }
 }
