@@ -567,6 +567,20 @@ size_t attn_prompt_kv_bytes(int n_kv, int d_head, int max_ctx)
     return (size_t)n_kv * tiles * KVT_POS * d_head * 4 * sizeof(_Float16);
 }
 
+static int attn_cus()
+{
+    static const int c = [] {
+        int d = 0, n = 0;
+        if (hipGetDevice(&d) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess ||
+            n < 1) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        return n;
+    }();
+    return c;
+}
+
 template <int DH>
 int launch_attn_prompt_dh(const AttnArgs &a, _Float16 *kv_hl, int last, hipStream_t s)
 {
@@ -591,8 +605,17 @@ int launch_attn_prompt(const AttnArgs &a, _Float16 *kv_hl, int last, hipStream_t
         return -4;
     if (a.split < 64 || a.split % KVT_POS || a.max_splits > ATT_MAX_MERGE) return -4;
     if (!kv_hl || last < 1 || last > a.max_ctx) return -4;
-    const int rc = a.d_head == 128 ? launch_attn_prompt_dh<128>(a, kv_hl, last, s)
-                                   : launch_attn_prompt_dh<64>(a, kv_hl, last, s);
+    // the pass's split: the longest multiple of the planned one that still
+    // gives every CU two work-groups (a 2048-token pass: one split, no
+    // merge; 512-token passes: 256-512 positions).  Fewer splits than
+    // planned always fit the partial buffers.
+    AttnArgs b = a;
+    const long blocks = (long)a.n_kv * ((a.n + 64 / G - 1) / (64 / G));
+    while (b.split * 2 <= a.max_ctx && blocks * ((last + 2 * b.split - 1) / (2 * b.split)) >= 2L * attn_cus())
+        b.split *= 2;
+    b.max_splits = (last + b.split - 1) / b.split;
+    const int rc = a.d_head == 128 ? launch_attn_prompt_dh<128>(b, kv_hl, last, s)
+                                   : launch_attn_prompt_dh<64>(b, kv_hl, last, s);
     if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
