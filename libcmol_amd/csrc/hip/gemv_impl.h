@@ -401,12 +401,30 @@ void k_gemv(GemvArgs a, GemvShape sh)
             for (int gi = 0; gi < NG; gi++)
                 xv[bi][gi] = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
         }
+        if constexpr (is_kquant(DT) || NG > 1) {
 #pragma unroll
-        for (int bi = 0; bi < 4; bi++) {
-            const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
-            const BlockScale bs = block_scale<DT>(dv[u], bi);
+            for (int bi = 0; bi < 4; bi++) {
+                const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
+                const BlockScale bs = block_scale<DT>(dv[u], bi);
 #pragma unroll
-            for (int gi = 0; gi < NG; gi++) mfma_block<DT>(acc[gi], xv[bi][gi], wv, bs);
+                for (int gi = 0; gi < NG; gi++) mfma_block<DT>(acc[gi], xv[bi][gi], wv, bs);
+            }
+        } else {
+            // four independent products, then the scale FMAs in block order
+            // (mfma_block's sums, without serialising the MFMAs on one
+            // result register)
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 cc[4];
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++)
+                cc[bi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[bi][0], deq_block<DT>(c0[u], c1[u], hv[u], bi), z,
+                                                                0, 0, 0);
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++) {
+                const BlockScale bs = block_scale<DT>(dv[u], bi);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[0][e] = fmaf(bs.s0, cc[bi][e], acc[0][e]);
+            }
         }
     };
     // rounds of U: while another round follows, slot u is refilled right
@@ -826,11 +844,31 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
     };
     auto compute = [&](int u, int i) {
         const int j = i / nq, q = i - j * nq;
+        // the quad's four operand reads go out together, ahead of the decode
+        f16x8 xv[4];
 #pragma unroll
-        for (int bi = 0; bi < 4; bi++) {
-            const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
-            const f16x8 xv = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
-            mfma_block<DT>(acc, xv, wv, block_scale<DT>(dv[u], bi));
+        for (int bi = 0; bi < 4; bi++) xv[bi] = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
+        if constexpr (is_kquant(DT)) {
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++) {
+                const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
+                mfma_block<DT>(acc, xv[bi], wv, block_scale<DT>(dv[u], bi));
+            }
+        } else {
+            // four independent products first, then the scale FMAs in block
+            // order (the same sums as mfma_block's, without serialising the
+            // MFMAs on one result register)
+            f32x4 cc[4];
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++)
+                cc[bi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[bi], deq_block<DT>(c0[u], c1[u], hv[u], bi), zero4,
+                                                                0, 0, 0);
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++) {
+                const BlockScale bs = block_scale<DT>(dv[u], bi);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = fmaf(bs.s0, cc[bi][e], acc[e]);
+            }
         }
         if (q == nq - 1) finish_tile(j);
     };
