@@ -105,10 +105,14 @@ def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
 @pytest.mark.parametrize("dtype,rows,cols,fold,n", [
     (2, 384, 2048, 1, 33), (2, 256, 2048, 1, 64), (2, 300, 2048, 1, 130), (8, 576, 576, 1, 200),
     (6, 320, 960, 1, 97), (6, 2560, 960, 1, 64), (2, 2048, 11008, 4, 65), (2, 3072, 2048, 4, 128),
-    (8, 200, 576, 8, 70), (6, 960, 960, 2, 96), (2, 37, 4096, 1, 40), (2, 512, 2048, 1, 512)])
+    (8, 200, 576, 8, 70), (6, 960, 960, 2, 96), (2, 37, 4096, 1, 40), (2, 512, 2048, 1, 512),
+    (6, 1664, 960, 2, 640), (8, 2176, 576, 1, 600), (2, 2100, 2048, 4, 700)])
 def test_gemm_tiled_matches_oracle(ctx, dtype, rows, cols, fold, n):
     """More than 32 vectors run the tiled MFMA GEMM (prompt prefill): partial
-    row and vector tiles, folded weights read in place, and padding blocks."""
+    row and vector tiles, folded weights read in place, and padding blocks.
+    Shapes with more than 128 tiles of 64 vectors x 128 rows take the
+    eight-wave work-groups (the last three), the others the four-wave ones;
+    k ranges of 960 and 576 end in partial quads."""
     raw = random_blocks(dtype, rows, cols, seed=rows * 5 + cols + n)
     x = np.random.default_rng(n + 1).standard_normal((n, cols)).astype(np.float32)
     t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
