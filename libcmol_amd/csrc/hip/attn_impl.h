@@ -270,8 +270,11 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
 //     head; the chunk's V rows are staged in LDS row-major (rows padded by
 //     two halves so that the eight-position column reads of the B operand
 //     fall in distinct banks) and gathered as B columns.
-// Every product is exact and every sum fp32.  Staged V is double-buffered,
-// so a chunk needs two barriers.  Same partial format as attn_split.
+// Every product is exact and every sum fp32.  V goes through one LDS buffer:
+// the chunk's V rows, loaded into registers during the previous chunk, are
+// written after the first barrier (every wave is then done with the previous
+// weighted sum), so a chunk needs two barriers and 21 KB of LDS (d_head
+// 128).  Same partial format as attn_split.
 template <int DH, typename M>
 __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp, int n)
 {
@@ -295,12 +298,11 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
 
     __shared__ float esh[ATT_MAX_G][CH];
     __shared__ __attribute__((aligned(16))) _Float16 ph[2][ATT_MAX_G][CH];
-    __shared__ __attribute__((aligned(16))) _Float16 vs[2][CH * RS];
-    // the query is read once, into the MFMA operand, before chunk 1 is
-    // staged: it lives in the second V buffer (LDS below 40 KB for d_head
-    // 128 keeps four work-groups on a CU)
+    __shared__ __attribute__((aligned(16))) _Float16 vs[CH * RS];
+    // the query is read once, into the MFMA operand, before chunk 0 is
+    // staged: it lives in the V buffer
     static_assert(ATT_MAX_G * DH * 4 <= CH * RS * 2, "query area");
-    float *qsh = (float *)vs[1];
+    float *qsh = (float *)vs;
     __shared__ float alpha_sh[ATT_MAX_G], m_sh[ATT_MAX_G], l_sh[ATT_MAX_G];
 
     const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
@@ -365,7 +367,7 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
 
     for (int c = 0; c < nch; c++) {
         const int ccnt = min(CH, cnt - c * CH);
-        _Float16 *vcur = vs[c & 1];
+        _Float16 *vcur = vs;
         // scores of positions 16w .. 16w+15: lane l holds position 16w + l%16
         // for rows 4(l/16) .. +3 (heads 2(l/16), 2(l/16)+1, high and low)
         f32x4 sc = zero4;
@@ -380,9 +382,9 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
                 if (h < G) esh[h][pp] = pp < ccnt ? (sc[2 * k] + sc[2 * k + 1] * (1.0f / 2048.0f)) * scale : -INFINITY;
             }
         }
+        __syncthreads();   // scores in LDS; every wave done with the last chunk's V
         stage_v(vcur);
         if (c + 1 < nch) load_v(c + 1);
-        __syncthreads();
         // online softmax: wave w owns heads w, w + 4; lane j holds position j
         for (int h = wid; h < G; h += NT / 64) {
             const float sv = esh[h][lane];
