@@ -401,7 +401,10 @@ void k_gemv(GemvArgs a, GemvShape sh)
             for (int gi = 0; gi < NG; gi++)
                 xv[bi][gi] = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
         }
-        if constexpr (is_kquant(DT) || NG > 1) {
+        // (four-wave instances with a deep ring keep the serial form: the
+        // extra result registers would cost them a wave per SIMD, e.g. the
+        // Q8_0 LM head 128 -> 140 VGPRs)
+        if constexpr (is_kquant(DT) || NG > 1 || (NW == 4 && U > 4)) {
 #pragma unroll
             for (int bi = 0; bi < 4; bi++) {
                 const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
