@@ -847,20 +847,23 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
     };
     auto compute = [&](int u, int i) {
         const int j = i / nq, q = i - j * nq;
-        // the quad's four operand reads go out together, ahead of the decode
-        f16x8 xv[4];
-#pragma unroll
-        for (int bi = 0; bi < 4; bi++) xv[bi] = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
-        if constexpr (is_kquant(DT)) {
+        if constexpr (DT != DT_Q4_0 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
 #pragma unroll
             for (int bi = 0; bi < 4; bi++) {
                 const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
-                mfma_block<DT>(acc, xv[bi], wv, block_scale<DT>(dv[u], bi));
+                const f16x8 xv = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
+                mfma_block<DT>(acc, xv, wv, block_scale<DT>(dv[u], bi));
             }
         } else {
-            // four independent products first, then the scale FMAs in block
+            // Q4_0 instances whose epilogue leaves room (elsewhere the extra
+            // registers push the kernel past 128 VGPRs, one work-group per CU
+            // instead of two): the quad's four operand reads go out together,
+            // then four independent products, then the scale FMAs in block
             // order (the same sums as mfma_block's, without serialising the
             // MFMAs on one result register)
+            f16x8 xv[4];
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++) xv[bi] = *(const f16x8 *)(abase + (size_t)(4 * q + bi) * 1024);
             f32x4 cc[4];
 #pragma unroll
             for (int bi = 0; bi < 4; bi++)
