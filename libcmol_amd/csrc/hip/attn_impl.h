@@ -268,8 +268,9 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
 //     step;
 //   * weighted sum: wave w owns dimensions w*d_head/4 .. +d_head/4 of every
 //     head; the chunk's V rows are staged in LDS row-major (rows padded by
-//     two halves so that the eight-position column reads of the B operand
-//     fall in distinct banks) and gathered as B columns.
+//     four halves) and each B column (one dimension, eight positions) comes
+//     from two transposing LDS reads (ds_read_b64_tr_b16) instead of eight
+//     16-bit reads.
 // Every product is exact and every sum fp32.  V goes through one LDS buffer:
 // the chunk's V rows, loaded into registers during the previous chunk, are
 // written after the first barrier (every wave is then done with the previous
@@ -285,7 +286,7 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
     constexpr int VPT = CH * PPP / NT;     // V pieces per thread per chunk
     constexpr int DW = DH / 4;             // dimensions per wave
     constexpr int DTW = DW / 16;           // 16-dimension MFMA tiles per wave
-    constexpr int RS = DH + 2;             // LDS row stride of the staged V (halves)
+    constexpr int RS = DH + 4;             // LDS row stride of the staged V (halves; rows 8-byte aligned)
     static_assert(DH >= 64 && DH % 64 == 0 && VPT >= 1, "shape");
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
     const int G = a.n_heads / a.n_kv;
@@ -422,10 +423,18 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
             if (rh >= G) pa = f16x8{};
 #pragma unroll
             for (int t = 0; t < DTW; t++) {
-                const _Float16 *col = vcur + pb * RS + d0 + 16 * t;
-                f16x8 bv;
-#pragma unroll
-                for (int e = 0; e < 8; e++) bv[e] = col[e * RS];
+                // B columns: lane (col, g) takes dimension d0 + 16t of
+                // positions pb .. pb+7, gathered by two transposing LDS reads:
+                // within each 16-lane group, lane s reads the four dimensions
+                // 4(s%4) .. +3 of the tile at position pb + s/4 (+4), and the
+                // read hands lane 4r+c element c of the lanes 4e+r
+                const int s16 = lane & 15;
+                const _Float16 *src = vcur + (pb + (s16 >> 2)) * RS + wid * DW + 16 * t + 4 * (s16 & 3);
+                typedef short s16x4 __attribute__((ext_vector_type(4)));
+                const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)src);
+                const s16x4 hi4 =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(src + 4 * RS));
+                const f16x8 bv = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
                 oc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bv, oc[t], 0, 0, 0);
             }
         }
