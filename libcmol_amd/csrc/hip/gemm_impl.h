@@ -1,13 +1,15 @@
 // gemm_impl.h — the prompt (prefill) GEMM: Y[n][rows] = X[n][K] . W^T for
 // many activation vectors (n = prompt tokens), instantiated per weight
-// format by gemm_q4.hip / gemm_q5.hip / gemm_q8.hip.
+// format by gemm_q4.hip / gemm_q5.hip / gemm_q8.hip / gemm_q4k.hip /
+// gemm_q6k.hip.
 //
 // One work-group computes a 64-vector x 128-row output tile (32 x 128 with
-// four waves where 64-vector tiles would leave half the CUs idle).  Its eight
-// waves form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31 (two groups
-// of 16, each with a 16-row high and a 16-row low operand block in LDS) and
-// output rows 32wn..32wn+31 (two 16-row "virtual tiles").  The k loop walks block quads
-// through a two-stage pipeline: the activation operand of quad kk+1 is
+// four waves where 64-vector tiles would leave half the CUs idle).  Its
+// eight waves form a 2 x 4 grid: wave (wm, wn) owns vectors 32wm..32wm+31
+// (two groups of 16, each with a 16-row high and a 16-row low operand block
+// in LDS) and output rows 32wn..32wn+31 (two 16-row "virtual tiles").  The
+// k loop walks block quads through a two-stage pipeline: the activation
+// operand of quad kk+1 is
 // copied into LDS with direct-to-LDS loads and each wave loads the weight
 // codes of its two virtual tiles for it into registers while quad kk is
 // contracted.  Two stages (64 KiB of LDS) keep two work-groups on a CU,
@@ -30,7 +32,7 @@
 
 struct GemmShape {
     int epi;
-    int mt;          // 64-vector tiles
+    int mt;          // vector tiles (GEMM_BM vectors each)
     int nt;          // 128-row tiles
     int vt;          // 16-row virtual tiles (ceil(rows / 16))
     int ga;          // XCD slices along the vector tiles (1, 2, 4, 8)
