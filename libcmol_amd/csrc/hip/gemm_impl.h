@@ -9,10 +9,9 @@
 // (two groups of 16, each with a 16-row high and a 16-row low operand block
 // in LDS) and output rows 32wn..32wn+31 (two 16-row "virtual tiles").  The
 // k loop walks block quads through a two-stage pipeline: the activation
-// operand of quad kk+1 is
-// copied into LDS with direct-to-LDS loads and each wave loads the weight
-// codes of its two virtual tiles for it into registers while quad kk is
-// contracted.  Two stages (64 KiB of LDS) keep two work-groups on a CU,
+// operand of quad kk+1 is copied into LDS with direct-to-LDS loads and each
+// wave loads the weight codes of its two virtual tiles for it into
+// registers while quad kk is contracted.  Two stages (64 KiB of LDS) keep two work-groups on a CU,
 // which hides more latency than a third stage in flight with one.
 // Weights of any fold are read in place: virtual tile V of part p gathers,
 // for column c', the codes of row 16V + c' from tile (16V + c') / R,
