@@ -893,6 +893,137 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
     }
 }
 
+// Batched matvec over one round of sixteen-wave work-groups for 17-32
+// vectors of an unsplit k range (the gate/up shape at 32 sessions), where
+// the kernel above would need a second round of work-groups.  A work-group
+// holds the operand of 16 vectors over the whole k range in LDS ([block]
+// [k-group][16 high rows, 16 low rows][16 B]); each wave streams one 16-row
+// tile.  Per block the low part's product joins the high part's MFMA sum
+// (codes times 2^-11 against the low part times 2^11, exact), so one decode
+// and one scale FMA per output serve 16 vectors.  Lane (c, g) ends with
+// row 16t + c of vectors 4g .. 4g+3.
+#define GB16_NW 16
+template <int DT, int U, int EPI>
+__global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int groups, int rblocks)
+{
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int BQ = a.w.block_quads, nblk = a.w.cols >> 5, T = a.w.row_tiles;
+    const int b = blockIdx.x;
+    const int vg = (b >> 3) % groups;
+    const int rb = (b / (8 * groups)) * 8 + (b & 7);
+    if (rb >= rblocks) return;
+    const int n = a.n, nrows = 2 * n, v0 = vg * 16;
+    (void)nblk;
+    const int tid = threadIdx.x, l = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // every block of every quad is staged (blocks past the matrix re-read
+    // the last one: they meet zero weights)
+    float *s_nrm = (float *)(smem + (size_t)BQ * 4 * 2048);
+    for (int pc = wid; pc < 8 * BQ; pc += GB16_NW) {
+        const int blk = min(pc >> 1, nblk - 1), kg = 2 * (pc & 1) + (l >> 5), r = l & 31;
+        const int row = min(2 * (v0 + (r & 15)) + (r >> 4), nrows - 1);
+        const uint8_t *src = (const uint8_t *)a.in.q + (((size_t)blk * 4 + kg) * nrows + row) * 16;
+        __builtin_amdgcn_global_load_lds((const gvoid_t *)src, (lvoid_t *)(smem + (size_t)pc * 1024), 16, 0, 0);
+    }
+    const int t = rb * GB16_NW + wid;
+    const int tt = t < T ? t : T - 1;
+    u32x4 c0[U], c1[U];
+    typename QScale<DT>::T dv[U];
+    uint32_t hv[U];
+    auto load_slot = [&](int u, int q) {
+        q = min(q, BQ - 1);
+        q_load<DT>(a.w, (size_t)tt * BQ + q, l & 15, l, c0[u], c1[u], dv[u], hv[u]);
+    };
+#pragma unroll
+    for (int u = 0; u < U; u++) load_slot(u, u);
+    // RMSNorm scale of vector v0 + w from its producer's partials (wave w),
+    // summed in the order k_gemv_b sums them
+    if (a.in.ss) {
+        const int v = min(v0 + wid, n - 1);
+        float sum = 0.0f;
+        for (int i = l; i < a.in.ss_count; i += 64) sum += a.in.ss[(size_t)v * a.in.ss_stride + i];
+        sum = wave_sum(sum);
+        if (l == 0) s_nrm[wid] = 1.0f / sqrtf(sum / (float)a.w.cols + a.in.eps);
+    }
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
+    __syncthreads();
+    const int g = l >> 4, cl = l & 15;
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc = z;
+    auto compute = [&](int u, int q) {
+        f16x8 xh[4], xl[4];
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            const uint8_t *p = smem + (size_t)(4 * q + bi) * 2048 + (g * 32 + cl) * 16;
+            xh[bi] = *(const f16x8 *)p;
+            xl[bi] = *(const f16x8 *)(p + 256);
+        }
+        f32x4 cc[4];
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            const f16x8 wv = deq_block<DT>(c0[u], c1[u], hv[u], bi);
+            const f16x8 wl = wv * (_Float16)LO_INV_SCALE;
+            cc[bi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[bi], wv, z, 0, 0, 0);
+            cc[bi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[bi], wl, cc[bi], 0, 0, 0);
+        }
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            const BlockScale bs = block_scale<DT>(dv[u], bi);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(bs.s0, cc[bi][e], acc[e]);
+        }
+    };
+    // the loop is uniform over the wave (every wave runs all BQ quads, a
+    // wave past the last tile on a valid tile's data) so every wait count
+    // is the same
+    for (int q0 = 0; q0 < BQ; q0 += U) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (q0 + u < BQ) compute(u, q0 + u);
+            load_slot(u, q0 + u + U);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int vl = 4 * g + e, v = v0 + vl;
+        const bool act = v < n && t < T;
+        float y = acc[e] * ACT_INV_SCALE;
+        if (a.in.ss) y *= s_nrm[vl];
+        epilogue<EPI>(a, t, cl, 16, act ? v : 0, act, y);
+    }
+}
+
+// Whether launch_gemv_b takes k_gemv_b16: 17-32 vectors, a 32-value block
+// format, the operand of 16 vectors over the whole k range in LDS, and a
+// plan of k_gemv_b without k split that needs more than one round of
+// resident work-groups (two per CU).
+static inline bool gb16_fits(const QTensor &w, int n, const GbShape &sh, int wgs)
+{
+    return !is_kquant(w.dtype) && n > 16 && n <= 32 && w.fold == 1 && sh.splits == 1 &&
+           (size_t)w.block_quads * 4 * 2048 + 64 <= 160 * 1024 && wgs > 2 * gemv_cus();
+}
+
+template <int DT, int EPI>
+static int launch_gemv_b16(const GemvArgs &a, hipStream_t s)
+{
+    constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
+    const size_t lds = (size_t)a.w.block_quads * 4 * 2048 + 64;
+    static const bool lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI>,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   160 * 1024) == hipSuccess;
+    if (!lds_ok) return -6;
+    const int groups = (a.n + 15) / 16, rblocks = (a.w.row_tiles + GB16_NW - 1) / GB16_NW;
+    const long blocks = (long)((rblocks + 7) / 8) * 8 * groups;
+    if (a.ev_start)
+        hipExtLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s,
+                              a.ev_start, a.ev_stop, 0, a, groups, rblocks);
+    else
+        hipLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s, a, groups,
+                           rblocks);
+    return 0;
+}
+
 template <int DT>
 static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
 {
@@ -901,6 +1032,17 @@ static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
     sh.epi = epi;
     sh.ss_count = a.in.ss ? a.in.ss_count : 0;
     const int wgs = gb_plan(a.w, a.n, sh);
+    if constexpr (!is_kquant(DT)) {
+        if (gb16_fits(a.w, a.n, sh, wgs)) {
+            switch (epi) {
+            case EPI_STORE: return launch_gemv_b16<DT, EPI_STORE>(a, s);
+            case EPI_RESID: return launch_gemv_b16<DT, EPI_RESID>(a, s);
+            case EPI_SWIGLU: return launch_gemv_b16<DT, EPI_SWIGLU>(a, s);
+            case EPI_QKV: return launch_gemv_b16<DT, EPI_QKV>(a, s);
+            default: return launch_gemv_b16<DT, EPI_LOGITS>(a, s);
+            }
+        }
+    }
     if (sh.splits > 1 && (!a.part || (size_t)sh.splits * a.n * a.w.rows > a.part_cap)) return -6;
     const long blocks = (long)((sh.rblocks * sh.splits + 7) / 8) * 8 * sh.groups;
     const size_t lds = (size_t)4 * sh.sq * 1024 + ((GB_VG * sh.ss_count + 3) & ~3) * 4 + GB_VG * 4;

@@ -137,11 +137,15 @@ def test_gemm_tiled_rmsnorm_prologue(ctx):
 
 @pytest.mark.parametrize("dtype,rows,cols,n", [
     (2, 3072, 2048, 32), (2, 2048, 11008, 32), (2, 22016, 2048, 32), (6, 960, 2560, 16),
-    (8, 576, 576, 24), (2, 300, 2048, 9), (6, 1600, 960, 16), (8, 4104, 576, 12)])
+    (8, 576, 576, 24), (2, 300, 2048, 9), (6, 1600, 960, 16), (8, 4104, 576, 12),
+    (2, 22016, 2048, 21), (8, 16404, 1024, 32), (6, 16400, 960, 32)])
 def test_gemv_batched_groups_match_oracle(ctx, dtype, rows, cols, n):
     """9..32 vectors: vector groups of 8, operand slices staged once per
     work-group, k splits summed by the finish kernel; partial row tiles and
-    partial vector groups included."""
+    partial vector groups included.  Unsplit shapes of 17-32 vectors that
+    need more than one round of work-groups (the 22016-row ones and the last
+    two) take the sixteen-wave kernel with vector groups of 16, including a
+    partial group, a partial row tile and a k range ending in a partial quad."""
     raw = random_blocks(dtype, rows, cols, seed=rows + 7 * cols + n)
     x = np.random.default_rng(n + 3).standard_normal((n, cols)).astype(np.float32)
     t = ctx.qtensor([raw], dtype, cols, [rows])
