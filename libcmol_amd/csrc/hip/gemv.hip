@@ -78,7 +78,10 @@ size_t gemv_part_floats(const QTensor &w, int n)
     if (!gemv_batched(w, n)) return 0;
     GbShape sh;
     gb_plan(w, n, sh);
-    return sh.splits > 1 ? (size_t)sh.splits * n * w.rows : 0;
+    size_t f = sh.splits > 1 ? (size_t)sh.splits * n * w.rows : 0;
+    Gb16Shape p;
+    if (gb16_plan(w, n, p) && p.splits > 1) f = std::max(f, (size_t)p.splits * n * w.rows);
+    return f;
 }
 
 // k-split finish: one wave per (64 rows, vector); lane l takes row 64*bx + l,

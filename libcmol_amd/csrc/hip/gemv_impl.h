@@ -904,24 +904,25 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
 // row 16t + c of vectors 4g .. 4g+3.
 #define GB16_NW 16
 template <int DT, int U, int EPI>
-__global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int groups, int rblocks)
+__global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int groups, int rblocks, int sq, int splits)
 {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int BQ = a.w.block_quads, nblk = a.w.cols >> 5, T = a.w.row_tiles;
     const int b = blockIdx.x;
     const int vg = (b >> 3) % groups;
-    const int rb = (b / (8 * groups)) * 8 + (b & 7);
-    if (rb >= rblocks) return;
+    const int rest = (b / (8 * groups)) * 8 + (b & 7);
+    if (rest >= rblocks * splits) return;
+    const int rb = rest % rblocks, ks = rest / rblocks;
+    const int q0 = ks * sq, nq = min(sq, BQ - q0);
     const int n = a.n, nrows = 2 * n, v0 = vg * 16;
-    (void)nblk;
     const int tid = threadIdx.x, l = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     // every block of every quad is staged (blocks past the matrix re-read
     // the last one: they meet zero weights)
-    float *s_nrm = (float *)(smem + (size_t)BQ * 4 * 2048);
-    for (int pc = wid; pc < 8 * BQ; pc += GB16_NW) {
-        const int blk = min(pc >> 1, nblk - 1), kg = 2 * (pc & 1) + (l >> 5), r = l & 31;
+    float *s_nrm = (float *)(smem + (size_t)sq * 4 * 2048);
+    for (int pc = wid; pc < 8 * nq; pc += GB16_NW) {
+        const int blk = min(4 * q0 + (pc >> 1), nblk - 1), kg = 2 * (pc & 1) + (l >> 5), r = l & 31;
         const int row = min(2 * (v0 + (r & 15)) + (r >> 4), nrows - 1);
         const uint8_t *src = (const uint8_t *)a.in.q + (((size_t)blk * 4 + kg) * nrows + row) * 16;
         __builtin_amdgcn_global_load_lds((const gvoid_t *)src, (lvoid_t *)(smem + (size_t)pc * 1024), 16, 0, 0);
@@ -932,14 +933,14 @@ __global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int group
     typename QScale<DT>::T dv[U];
     uint32_t hv[U];
     auto load_slot = [&](int u, int q) {
-        q = min(q, BQ - 1);
-        q_load<DT>(a.w, (size_t)tt * BQ + q, l & 15, l, c0[u], c1[u], dv[u], hv[u]);
+        q = min(q, nq - 1);
+        q_load<DT>(a.w, (size_t)tt * BQ + q0 + q, l & 15, l, c0[u], c1[u], dv[u], hv[u]);
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load_slot(u, u);
     // RMSNorm scale of vector v0 + w from its producer's partials (wave w),
     // summed in the order k_gemv_b sums them
-    if (a.in.ss) {
+    if (a.in.ss && splits == 1) {
         const int v = min(v0 + wid, n - 1);
         float sum = 0.0f;
         for (int i = l; i < a.in.ss_count; i += 64) sum += a.in.ss[(size_t)v * a.in.ss_stride + i];
@@ -977,50 +978,88 @@ __global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int group
     // the loop is uniform over the wave (every wave runs all BQ quads, a
     // wave past the last tile on a valid tile's data) so every wait count
     // is the same
-    for (int q0 = 0; q0 < BQ; q0 += U) {
+    for (int i0 = 0; i0 < nq; i0 += U) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (q0 + u < BQ) compute(u, q0 + u);
-            load_slot(u, q0 + u + U);
+            if (i0 + u < nq) compute(u, i0 + u);
+            load_slot(u, i0 + u + U);
         }
     }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int vl = 4 * g + e, v = v0 + vl;
-        const bool act = v < n && t < T;
+        const bool act = v < n && t < T && t * 16 + cl < a.w.rows;
         float y = acc[e] * ACT_INV_SCALE;
+        if (splits > 1) {
+            // k-split partial sums: k_gemv_b_finish adds them and runs the
+            // epilogue, as for k_gemv_b
+            if (act) a.part[((size_t)ks * n + v) * a.w.rows + t * 16 + cl] = y;
+            continue;
+        }
         if (a.in.ss) y *= s_nrm[vl];
         epilogue<EPI>(a, t, cl, 16, act ? v : 0, act, y);
     }
 }
 
-// Whether launch_gemv_b takes k_gemv_b16: 17-32 vectors, a 32-value block
-// format, the operand of 16 vectors over the whole k range in LDS, and a
-// plan of k_gemv_b without k split that needs more than one round of
-// resident work-groups (two per CU).
-static inline bool gb16_fits(const QTensor &w, int n, const GbShape &sh, int wgs)
+// The plan of k_gemv_b16: 17-32 vectors of a 32-value block format in two
+// groups of 16; sixteen-wave work-groups, one per CU resident.  Taken where
+// k_gemv_b's own plan
+//   * needs more than one round of work-groups without a k split (gate/up
+//     at 32 sessions: 688 work-groups for 512 resident), or
+//   * splits a long k range into slices of 8 quads or more (down at 32
+//     sessions: 6 slices of 15 quads); k_gemv_b16 then splits it so that its
+//     work-groups fill the CUs once (15 slices of 6 quads) and
+//     k_gemv_b_finish adds the slices as for k_gemv_b.
+// CMOL_B16_SPLITS=<s> forces it with s slices (measurements).
+struct Gb16Shape {
+    int groups, rblocks, sq, splits;
+};
+
+static inline bool gb16_plan(const QTensor &w, int n, Gb16Shape &p)
 {
-    return !is_kquant(w.dtype) && n > 16 && n <= 32 && w.fold == 1 && sh.splits == 1 &&
-           (size_t)w.block_quads * 4 * 2048 + 64 <= 160 * 1024 && wgs > 2 * gemv_cus();
+    if (is_kquant(w.dtype) || n <= 16 || n > 32 || w.fold != 1) return false;
+    static const int forced = [] {
+        const char *e = getenv("CMOL_B16_SPLITS");
+        return e ? atoi(e) : 0;
+    }();
+    const int BQ = w.block_quads;
+    p.groups = (n + 15) / 16;
+    p.rblocks = (w.row_tiles + GB16_NW - 1) / GB16_NW;
+    int s = 1;
+    if (forced > 0) {
+        s = forced;
+    } else {
+        GbShape sh;
+        const int wgs = gb_plan(w, n, sh);
+        if (sh.splits == 1) {
+            if (wgs <= 2 * gemv_cus()) return false;
+        } else {
+            if (sh.sq < 8) return false;
+            s = max(1, gemv_cus() / (p.groups * p.rblocks));
+        }
+    }
+    p.sq = (BQ + min(s, BQ) - 1) / min(s, BQ);
+    p.splits = (BQ + p.sq - 1) / p.sq;
+    return (size_t)p.sq * 4 * 2048 + 64 <= 160 * 1024;
 }
 
 template <int DT, int EPI>
-static int launch_gemv_b16(const GemvArgs &a, hipStream_t s)
+static int launch_gemv_b16(const GemvArgs &a, const Gb16Shape &p, hipStream_t s)
 {
     constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
-    const size_t lds = (size_t)a.w.block_quads * 4 * 2048 + 64;
+    const size_t lds = (size_t)p.sq * 4 * 2048 + 64;
     static const bool lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI>,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    160 * 1024) == hipSuccess;
     if (!lds_ok) return -6;
-    const int groups = (a.n + 15) / 16, rblocks = (a.w.row_tiles + GB16_NW - 1) / GB16_NW;
-    const long blocks = (long)((rblocks + 7) / 8) * 8 * groups;
+    const long blocks = (long)((p.rblocks * p.splits + 7) / 8) * 8 * p.groups;
+    const bool split = p.splits > 1;
     if (a.ev_start)
         hipExtLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s,
-                              a.ev_start, a.ev_stop, 0, a, groups, rblocks);
+                              a.ev_start, split ? nullptr : a.ev_stop, 0, a, p.groups, p.rblocks, p.sq, p.splits);
     else
-        hipLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s, a, groups,
-                           rblocks);
+        hipLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s, a,
+                           p.groups, p.rblocks, p.sq, p.splits);
     return 0;
 }
 
@@ -1033,13 +1072,19 @@ static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
     sh.ss_count = a.in.ss ? a.in.ss_count : 0;
     const int wgs = gb_plan(a.w, a.n, sh);
     if constexpr (!is_kquant(DT)) {
-        if (gb16_fits(a.w, a.n, sh, wgs)) {
+        Gb16Shape p;
+        if (gb16_plan(a.w, a.n, p)) {
+            if (p.splits > 1) {
+                if (!a.part || (size_t)p.splits * a.n * a.w.rows > a.part_cap) return -6;
+                const int rc = launch_gemv_b16<DT, EPI_STORE>(a, p, s);
+                return rc ? rc : launch_gemv_b_finish(a, epi, p.splits, sh.ss_count, s);
+            }
             switch (epi) {
-            case EPI_STORE: return launch_gemv_b16<DT, EPI_STORE>(a, s);
-            case EPI_RESID: return launch_gemv_b16<DT, EPI_RESID>(a, s);
-            case EPI_SWIGLU: return launch_gemv_b16<DT, EPI_SWIGLU>(a, s);
-            case EPI_QKV: return launch_gemv_b16<DT, EPI_QKV>(a, s);
-            default: return launch_gemv_b16<DT, EPI_LOGITS>(a, s);
+            case EPI_STORE: return launch_gemv_b16<DT, EPI_STORE>(a, p, s);
+            case EPI_RESID: return launch_gemv_b16<DT, EPI_RESID>(a, p, s);
+            case EPI_SWIGLU: return launch_gemv_b16<DT, EPI_SWIGLU>(a, p, s);
+            case EPI_QKV: return launch_gemv_b16<DT, EPI_QKV>(a, p, s);
+            default: return launch_gemv_b16<DT, EPI_LOGITS>(a, p, s);
             }
         }
     }
