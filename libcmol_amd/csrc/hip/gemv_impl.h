@@ -258,6 +258,8 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
 // exceeds the LDS budget); the NW waves split every k part into runs of qpc
 // quads, and each wave streams its weight quads through a ring of U
 // in-flight loads (one coalesced 16/32-byte load per lane per quad).
+// DIRECT (one group, fold 1): no operand copy; each ring slot also loads
+// the quad's four operand pieces of the lane from global memory.
 //
 // MFMA A rows: row 2(vF + p) + h is the high (h = 0) or scaled low (h = 1)
 // f16 part of vector v restricted to k part p; column c of the tile holds
@@ -273,11 +275,12 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
 // without spilling and are held there (six waves per SIMD, six work-groups
 // per CU): pick_nw gives them matrices with more tiles than eight-wave
 // groups can keep resident at once.
-template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI>
+template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI, bool DIRECT = false>
 __global__ __launch_bounds__(NW * 64)
-__attribute__((amdgpu_waves_per_eu(DT == DT_Q4_0 && NW == 4 && NG == 1 && U == 4 && EPI != EPI_QKV ? 6 : 1)))
+__attribute__((amdgpu_waves_per_eu(DT == DT_Q4_0 && NW == 4 && NG == 1 && U == 4 && EPI != EPI_QKV && !DIRECT ? 6 : 1)))
 void k_gemv(GemvArgs a, GemvShape sh)
 {
+    static_assert(!DIRECT || (NG == 1 && !CHUNKED), "direct operand: one group, no chunks");
     // launch arguments needed before the weight loads go out, fetched in
     // one round trip
     sgpr_pin(a.w.qs);
@@ -329,7 +332,7 @@ void k_gemv(GemvArgs a, GemvShape sh)
     epi_pre_load(a, epi, pv, prow, pact, pre);
 
     // ---- 1. operand and norm partials into LDS (issued first) ----
-    if constexpr (!CHUNKED) stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
+    if constexpr (!CHUNKED && !DIRECT) stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
     if (a.in.ss) stage_ss_dma<NW>(a.in.ss, a.in.ss_stride, a.in.ss_count, n, s_ss, wid, l);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -339,13 +342,25 @@ void k_gemv(GemvArgs a, GemvShape sh)
     u32x4 c0[U], c1[U];
     typename QScale<DT>::T dv[U];
     uint32_t hv[U];
+    // direct operand (fold 1, one group): the slot also holds the quad's four
+    // operand pieces of this lane, read from global memory (L2) in the
+    // layout a staged copy would have; A rows past the batch re-read the
+    // last vector's row (their outputs are discarded)
+    f16x8 xo[DIRECT ? U : 1][4];
+    const uint32_t xoff = DIRECT ? (uint32_t)(((l >> 4) * 2 * n + min(l & 15, 2 * n - 1)) * 16) : 0u;
     auto quad_of = [&](int i) {
         i = min(i, len - 1);
         const int c = CHUNKED ? i / qpc : 0;
         return min(c * cq + wid * qpc + (i - c * qpc), BQ - 1);
     };
     auto load_slot = [&](int u, int i) {
-        q_load<DT>(a.w, cell0 + quad_of(i), l & 15, l, c0[u], c1[u], dv[u], hv[u]);
+        const int qd = quad_of(i);
+        q_load<DT>(a.w, cell0 + qd, l & 15, l, c0[u], c1[u], dv[u], hv[u]);
+        if constexpr (DIRECT) {
+#pragma unroll
+            for (int bi = 0; bi < 4; bi++)
+                xo[u][bi] = ldg((const f16x8 *)((const uint8_t *)a.in.q + (uint32_t)(4 * qd + bi) * (uint32_t)vb + xoff));
+        }
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load_slot(u, u);
@@ -353,10 +368,15 @@ void k_gemv(GemvArgs a, GemvShape sh)
 
     // ---- 3. zero padding blocks and the zero slot, then wait for the copies
     // (loads retire in issue order: every load but the ring's) and meet ----
-    if constexpr (!CHUNKED) lds_zero<NW>(s_op + nblk * vb, sh.zslot + 16 - nblk * vb, threadIdx.x);
-    else lds_zero<NW>(s_op + sh.zslot, 16, threadIdx.x);
+    if constexpr (DIRECT) {
+    } else if constexpr (!CHUNKED) {
+        lds_zero<NW>(s_op + nblk * vb, sh.zslot + 16 - nblk * vb, threadIdx.x);
+    } else {
+        lds_zero<NW>(s_op + sh.zslot, 16, threadIdx.x);
+    }
     // load instructions per ring slot
-    constexpr int LPS = q_loads<DT>();
+    constexpr int LPS = q_loads<DT>() + (DIRECT ? 4 : 0);
+    static_assert(LPS * U <= 63, "ring loads beyond the vector memory counter");
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(LPS * U));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -398,8 +418,10 @@ void k_gemv(GemvArgs a, GemvShape sh)
 #pragma unroll
         for (int bi = 0; bi < 4; bi++) {
 #pragma unroll
-            for (int gi = 0; gi < NG; gi++)
-                xv[bi][gi] = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
+            for (int gi = 0; gi < NG; gi++) {
+                if constexpr (DIRECT) xv[bi][gi] = xo[u][bi];
+                else xv[bi][gi] = *(const f16x8 *)(s_op + abase[gi] + (4 * lq + bi) * astride[gi]);
+            }
         }
         // (four-wave instances with a deep ring keep the serial form: the
         // extra result registers would cost them a wave per SIMD, e.g. the
@@ -567,8 +589,18 @@ static inline int pick_nw(int tiles, int quads, bool four_held)
 
 static inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
-// LDS budget of one work-group.
-#define GEMV_LDS_BUDGET (64 * 1024)
+// LDS budget of one work-group: 80 KB keeps two resident per CU.  A grid of
+// at most one work-group per CU may take most of the CU's LDS.  An operand
+// beyond the budget is staged in chunks, each a barrier-separated round
+// trip, or (one operand group, grid of at most one work-group per CU) read
+// by the waves straight from L2.  CMOL_GEMV_LDS_KB overrides the budget for
+// measurements.
+static inline int gemv_lds_budget(int wgs)
+{
+    static const int kb = gb_env_int("CMOL_GEMV_LDS_KB", 0);
+    if (getenv("CMOL_GEMV_LDS_KB")) return kb * 1024;
+    return wgs <= gemv_cus() ? 156 * 1024 : 80 * 1024;
+}
 
 // Chooses quads per wave per chunk and the LDS areas; returns the dynamic
 // LDS bytes or -1 when the operand cannot be staged (`chunked` is set when
@@ -580,7 +612,7 @@ static inline int plan_gemv(const GemvArgs &a, int nw, GemvShape &sh, bool &chun
     sh.ss_bytes = a.in.ss ? round_up(a.n * a.in.ss_count * 4, 16) : 0;
     const int nrm = round_up(a.n * 4, 16);
     const int red = nw * a.n * 64;   // per-wave useful entries (16 columns x n floats)
-    const int cap = GEMV_LDS_BUDGET - sh.ss_bytes - nrm - red - 16;
+    const int cap = gemv_lds_budget(a.w.row_tiles) - sh.ss_bytes - nrm - red - 16;
     const long full = (long)F * 4 * BQ * vb;
     if (full <= cap) {
         chunked = false;
@@ -608,6 +640,7 @@ template <typename K>
 static void gemv_go(K kern, const GemvArgs &a, const GemvShape &sh, int lds, int nw, hipStream_t s)
 {
     const dim3 grid(a.w.row_tiles), block(nw * 64);
+    if (lds > 64 * 1024) hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (a.ev_start) hipExtLaunchKernelGGL(kern, grid, block, lds, s, a.ev_start, a.ev_stop, 0, a, sh);
     else hipLaunchKernelGGL(kern, grid, block, lds, s, a, sh);
 }
@@ -652,6 +685,26 @@ static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
     const int lds = plan_gemv(a, NW, sh, chunked);
     if (lds < 0) return -6;
     using RG = GemvRing<DT>;
+    // an operand beyond the budget on a grid of at most one work-group per
+    // CU: each wave reads its own quads' operand from L2 in its weight ring
+    // (no chunk barriers; every work-group reads the whole operand once, as
+    // the chunked copy does)
+    if constexpr (NG == 1) {
+        static const bool direct_on = [] {
+            const char *e = getenv("CMOL_GEMV_DIRECT");   // measurements
+            return !(e && e[0] == '0');
+        }();
+        if (chunked && direct_on && a.w.fold == 1 && a.w.row_tiles <= gemv_cus()) {
+            sh.qpc = (a.w.block_quads + NW - 1) / NW;
+            sh.zslot = 0;
+            sh.op_bytes = 16;
+            const int dl = sh.op_bytes + sh.ss_bytes + round_up(a.n * 4, 16) + NW * a.n * 64;
+            // a four-deep ring (eight-deep measured slower: 2048x11008 at n=8
+            // 12.5 vs 10.3 us); sixteen waves have 128 VGPRs a lane: two-deep
+            gemv_go(k_gemv<DT, NW, 1, false, NW >= 16 ? 2 : RG::S, -1, true>, a, sh, dl, NW, s);
+            return 0;
+        }
+    }
     const int len = chunked ? ((a.w.block_quads + sh.qpc * NW - 1) / (sh.qpc * NW)) * sh.qpc : sh.qpc;
     // the decode shape (one operand group, operand staged whole; residual
     // epilogues take no RMSNorm there) runs the epilogue-specialised kernel

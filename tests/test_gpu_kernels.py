@@ -22,7 +22,7 @@ def assert_close(got, want, what):
 
 @pytest.fixture(scope="module")
 def ctx(gpu):
-    c = gpu.Ctx(1 << 30)
+    c = gpu.Ctx(2 << 30)   # one bump arena for the module's tensors
     yield c
     c.close()
 
@@ -90,10 +90,14 @@ def test_gemv_matches_oracle(ctx, dtype, rows, cols, fold):
 @pytest.mark.parametrize("dtype,rows,cols,fold,n", [
     (2, 256, 2048, 1, 3), (2, 256, 2048, 1, 8), (2, 128, 11008, 1, 8), (2, 200, 2048, 1, 17),
     (8, 96, 960, 1, 32), (6, 160, 2560, 1, 16), (2, 512, 2048, 4, 2), (2, 512, 2048, 4, 4),
-    (2, 64, 2048, 2, 4), (8, 48, 576, 8, 2)])
+    (2, 64, 2048, 2, 4), (8, 48, 576, 8, 2),
+    # operands beyond the LDS budget on grids of at most one work-group per
+    # CU: read by the waves straight from L2 (partial row tiles included)
+    (8, 160, 8192, 1, 8), (6, 100, 11008, 1, 5), (2, 70, 16384, 1, 7), (2, 2048, 11008, 1, 6)])
 def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
     """Several activation vectors per launch (multi-session decode), including
-    operands staged in chunks (n * cols too large for one LDS copy)."""
+    operands staged in chunks or read from L2 (n * cols too large for one LDS
+    copy)."""
     raw = random_blocks(dtype, rows, cols, seed=rows * 3 + cols + n)
     x = np.random.default_rng(n).standard_normal((n, cols)).astype(np.float32)
     t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
@@ -169,17 +173,20 @@ def test_gemv_batched_groups_rmsnorm(ctx):
         assert_close(got, want, f"batched gemv rmsnorm {rows}x{cols} n {n}")
 
 
-def test_gemv_rmsnorm_prologue(ctx):
-    rows, cols, dtype = 256, 2048, 2
-    raw = random_blocks(dtype, rows, cols, seed=9)
+@pytest.mark.parametrize("rows,cols,n", [(256, 2048, 1), (192, 11008, 8)])
+def test_gemv_rmsnorm_prologue(ctx, rows, cols, n):
+    """RMSNorm scale of each vector from the staged sum-of-squares partials
+    (n=8 over 11008 inputs: operand read from L2)."""
+    dtype = 2
+    raw = random_blocks(dtype, rows, cols, seed=9 + n)
     rng = np.random.default_rng(3)
-    x = (rng.standard_normal(cols) * 3).astype(np.float32)
+    x = (rng.standard_normal((n, cols)) * 3).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
     t = ctx.qtensor([raw], dtype, cols, [rows])
-    got = ctx.gemm(t, x, norm_w=w, eps=1e-6)[0]
-    xn = O.rms_norm(x, w, 1e-6)
-    want = O.matmul(raw, xn, rows, cols, dtype, O.AVX512)[:, 0]
-    assert_close(got, want, "gemv with RMSNorm prologue")
+    got = ctx.gemm(t, x, norm_w=w, eps=1e-6)
+    xn = np.stack([O.rms_norm(xi, w, 1e-6) for xi in x])
+    want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"gemv with RMSNorm prologue n {n}")
 
 
 def test_gemv_reference_kats(ctx):
@@ -296,7 +303,7 @@ def test_kquant_upload_concat_interleave_chunked(ctx, dtype):
     (64, 256, 1, 1), (2048, 2048, 4, 1), (3072, 2048, 4, 1), (11008, 2048, 1, 1), (2048, 11008, 4, 1),
     (300, 1024, 8, 1), (96, 768, 2, 1), (256, 2048, 1, 3), (512, 2048, 4, 2), (256, 2048, 1, 8),
     (300, 2048, 1, 17), (2048, 11008, 1, 32), (384, 2048, 1, 40), (2048, 11008, 4, 65),
-    (300, 2048, 1, 130)])
+    (300, 2048, 1, 130), (2048, 11008, 1, 8), (90, 16384, 1, 5)])
 def test_kquant_gemv_gemm_match_oracle(ctx, dtype, rows, cols, fold, n):
     """Q4_K / Q6_K through the matvec (n <= 8), the vector-group kernel
     (9..32) and the tiled GEMM (> 32), folded and unfolded, against the
