@@ -640,7 +640,11 @@ template <typename K>
 static void gemv_go(K kern, const GemvArgs &a, const GemvShape &sh, int lds, int nw, hipStream_t s)
 {
     const dim3 grid(a.w.row_tiles), block(nw * 64);
-    if (lds > 64 * 1024) hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    // a refused attribute skips the launch; launch_gemv reports it
+    // through hipGetLastError
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+        return;
     if (a.ev_start) hipExtLaunchKernelGGL(kern, grid, block, lds, s, a.ev_start, a.ev_stop, 0, a, sh);
     else hipLaunchKernelGGL(kern, grid, block, lds, s, a, sh);
 }
