@@ -960,8 +960,8 @@ __global__ __launch_bounds__(GB_NW * 64) void k_gemv_b(GemvArgs a, GbShape sh)
 // and one scale FMA per output serve 16 vectors.  Lane (c, g) ends with
 // row 16t + c of vectors 4g .. 4g+3.
 #define GB16_NW 16
-template <int DT, int U, int EPI>
-__global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int groups, int rblocks, int sq, int splits)
+template <int DT, int U, int EPI, int NWB = GB16_NW>
+__global__ __launch_bounds__(NWB * 64) void k_gemv_b16(GemvArgs a, int groups, int rblocks, int sq, int splits)
 {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -978,13 +978,13 @@ __global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int group
     // every block of every quad is staged (blocks past the matrix re-read
     // the last one: they meet zero weights)
     float *s_nrm = (float *)(smem + (size_t)sq * 4 * 2048);
-    for (int pc = wid; pc < 8 * nq; pc += GB16_NW) {
+    for (int pc = wid; pc < 8 * nq; pc += NWB) {
         const int blk = min(4 * q0 + (pc >> 1), nblk - 1), kg = 2 * (pc & 1) + (l >> 5), r = l & 31;
         const int row = min(2 * (v0 + (r & 15)) + (r >> 4), nrows - 1);
         const uint8_t *src = (const uint8_t *)a.in.q + (((size_t)blk * 4 + kg) * nrows + row) * 16;
         __builtin_amdgcn_global_load_lds((const gvoid_t *)src, (lvoid_t *)(smem + (size_t)pc * 1024), 16, 0, 0);
     }
-    const int t = rb * GB16_NW + wid;
+    const int t = rb * NWB + wid;
     const int tt = t < T ? t : T - 1;
     u32x4 c0[U], c1[U];
     typename QScale<DT>::T dv[U];
@@ -995,14 +995,16 @@ __global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int group
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load_slot(u, u);
-    // RMSNorm scale of vector v0 + w from its producer's partials (wave w),
-    // summed in the order k_gemv_b sums them
+    // RMSNorm scale of vector v0 + j from its producer's partials (wave
+    // j mod NWB), summed in the order k_gemv_b sums them
     if (a.in.ss && splits == 1) {
-        const int v = min(v0 + wid, n - 1);
-        float sum = 0.0f;
-        for (int i = l; i < a.in.ss_count; i += 64) sum += a.in.ss[(size_t)v * a.in.ss_stride + i];
-        sum = wave_sum(sum);
-        if (l == 0) s_nrm[wid] = 1.0f / sqrtf(sum / (float)a.w.cols + a.in.eps);
+        for (int j = wid; j < 16; j += NWB) {
+            const int v = min(v0 + j, n - 1);
+            float sum = 0.0f;
+            for (int i = l; i < a.in.ss_count; i += 64) sum += a.in.ss[(size_t)v * a.in.ss_stride + i];
+            sum = wave_sum(sum);
+            if (l == 0) s_nrm[j] = 1.0f / sqrtf(sum / (float)a.w.cols + a.in.eps);
+        }
     }
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
     __syncthreads();
@@ -1070,6 +1072,7 @@ __global__ __launch_bounds__(GB16_NW * 64) void k_gemv_b16(GemvArgs a, int group
 // CMOL_B16_SPLITS=<s> forces it with s slices (measurements).
 struct Gb16Shape {
     int groups, rblocks, sq, splits;
+    int nw;   // waves per work-group (12 or 16)
 };
 
 static inline bool gb16_plan(const QTensor &w, int n, Gb16Shape &p)
@@ -1079,9 +1082,12 @@ static inline bool gb16_plan(const QTensor &w, int n, Gb16Shape &p)
         const char *e = getenv("CMOL_B16_SPLITS");
         return e ? atoi(e) : 0;
     }();
+    static const int nw_env = [] {
+        const char *e = getenv("CMOL_B16_WAVES");   // measurements: 12 or 16
+        return e ? atoi(e) : 0;
+    }();
     const int BQ = w.block_quads;
     p.groups = (n + 15) / 16;
-    p.rblocks = (w.row_tiles + GB16_NW - 1) / GB16_NW;
     int s = 1;
     if (forced > 0) {
         s = forced;
@@ -1092,32 +1098,46 @@ static inline bool gb16_plan(const QTensor &w, int n, Gb16Shape &p)
             if (wgs <= 2 * gemv_cus()) return false;
         } else {
             if (sh.sq < 8) return false;
-            s = max(1, gemv_cus() / (p.groups * p.rblocks));
+            s = max(1, gemv_cus() / (p.groups * ((w.row_tiles + GB16_NW - 1) / GB16_NW)));
         }
     }
     p.sq = (BQ + min(s, BQ) - 1) / min(s, BQ);
     p.splits = (BQ + p.sq - 1) / p.sq;
+    // twelve-wave work-groups where the unsplit grid then still runs in one
+    // round (SmolLM3-3B gate/up at n=32: 230 work-groups instead of 172 on
+    // 256 CUs, 16.9 vs 20.1 us); the k-split shapes keep sixteen (down:
+    // 15.7 vs 17.0 us)
+    const int r12 = (w.row_tiles + 11) / 12;
+    p.nw = nw_env == 12 || nw_env == 16 ? nw_env
+           : (p.splits == 1 && p.groups * r12 <= gemv_cus()) ? 12 : GB16_NW;
+    p.rblocks = (w.row_tiles + p.nw - 1) / p.nw;
     return (size_t)p.sq * 4 * 2048 + 64 <= 160 * 1024;
 }
 
-template <int DT, int EPI>
-static int launch_gemv_b16(const GemvArgs &a, const Gb16Shape &p, hipStream_t s)
+template <int DT, int EPI, int NWB>
+static int launch_gemv_b16_nw(const GemvArgs &a, const Gb16Shape &p, hipStream_t s)
 {
     constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
     const size_t lds = (size_t)p.sq * 4 * 2048 + 64;
-    static const bool lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI>,
+    static const bool lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI, NWB>,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    160 * 1024) == hipSuccess;
     if (!lds_ok) return -6;
     const long blocks = (long)((p.rblocks * p.splits + 7) / 8) * 8 * p.groups;
     const bool split = p.splits > 1;
     if (a.ev_start)
-        hipExtLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s,
+        hipExtLaunchKernelGGL((k_gemv_b16<DT, U, EPI, NWB>), dim3((unsigned)blocks), dim3(NWB * 64), lds, s,
                               a.ev_start, split ? nullptr : a.ev_stop, 0, a, p.groups, p.rblocks, p.sq, p.splits);
     else
-        hipLaunchKernelGGL((k_gemv_b16<DT, U, EPI>), dim3((unsigned)blocks), dim3(GB16_NW * 64), lds, s, a,
+        hipLaunchKernelGGL((k_gemv_b16<DT, U, EPI, NWB>), dim3((unsigned)blocks), dim3(NWB * 64), lds, s, a,
                            p.groups, p.rblocks, p.sq, p.splits);
     return 0;
+}
+
+template <int DT, int EPI>
+static int launch_gemv_b16(const GemvArgs &a, const Gb16Shape &p, hipStream_t s)
+{
+    return p.nw == 12 ? launch_gemv_b16_nw<DT, EPI, 12>(a, p, s) : launch_gemv_b16_nw<DT, EPI, GB16_NW>(a, p, s);
 }
 
 template <int DT>
