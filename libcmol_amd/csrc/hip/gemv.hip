@@ -86,6 +86,10 @@ size_t gemv_part_floats(const QTensor &w, int n)
 
 // k-split finish: one wave per (64 rows, vector); lane l takes row 64*bx + l,
 // so the lanes of a 16-row tile are a 16-lane group, as the epilogues need.
+// The epilogue's own inputs and the first FS slices' partial sums are
+// loaded together, unconditionally (rows past the matrix re-read the last
+// one), so the kernel waits for one round trip before the epilogue.
+#define FS 16
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, int ss_count)
 {
@@ -93,6 +97,14 @@ __global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, i
     const int v = blockIdx.y, l = threadIdx.x & 63;
     const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + l;
     if ((row & ~63) >= a.w.rows) return;   // whole waves past the matrix
+    const bool act = row < a.w.rows;
+    EpiPre pre;
+    epi_pre_load(a, EPI, v, row, act, pre);
+    const float *pp = a.part + (size_t)v * a.w.rows + min(row, a.w.rows - 1);
+    const size_t kstride = (size_t)a.n * a.w.rows;
+    float pv[FS];
+#pragma unroll
+    for (int k = 0; k < FS; k++) pv[k] = pp[(size_t)min(k, splits - 1) * kstride];
     float nrm = 1.0f;
     if (ss_count) {
         float s = 0.0f;
@@ -100,13 +112,17 @@ __global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, i
         s = wave_sum(s);
         nrm = 1.0f / sqrtf(s / (float)a.w.cols + a.in.eps);
     }
-    const bool act = row < a.w.rows;
+    epi_pre_cs(a, EPI, row, act, pre);
+    // slices added in ascending order
     float y = 0.0f;
-    if (act)
-        for (int k = 0; k < splits; k++) y += a.part[((size_t)k * a.n + v) * a.w.rows + row];
+#pragma unroll
+    for (int k = 0; k < FS; k++)
+        if (k < splits) y += pv[k];
+    for (int k = FS; k < splits; k++) y += pp[(size_t)k * kstride];
     y *= nrm;
-    epilogue<EPI>(a, row >> 4, row & 15, 16, v, act, y);
+    epilogue<EPI>(a, row >> 4, row & 15, 16, v, act, y, true, pre);
 }
+#undef FS
 
 int launch_gemv_b_finish(const GemvArgs &a, int epi, int splits, int ss_count, hipStream_t s)
 {
