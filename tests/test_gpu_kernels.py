@@ -93,7 +93,9 @@ def test_gemv_matches_oracle(ctx, dtype, rows, cols, fold):
     (2, 64, 2048, 2, 4), (8, 48, 576, 8, 2),
     # operands beyond the LDS budget on grids of at most one work-group per
     # CU: read by the waves straight from L2 (partial row tiles included)
-    (8, 160, 8192, 1, 8), (6, 100, 11008, 1, 5), (2, 70, 16384, 1, 7), (2, 2048, 11008, 1, 6)])
+    (8, 160, 8192, 1, 8), (6, 100, 11008, 1, 5), (2, 70, 16384, 1, 7), (2, 2048, 11008, 1, 6),
+    # more row tiles than CUs with such an operand: staged in chunks
+    (2, 4112, 11008, 1, 8), (8, 4100, 8192, 1, 3)])
 def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
     """Several activation vectors per launch (multi-session decode), including
     operands staged in chunks or read from L2 (n * cols too large for one LDS
