@@ -542,6 +542,9 @@ struct Batch {
     unsigned long long *h_argmax = nullptr;   // pinned [cap][ARGMAX_SLOTS]
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
+    // the shared batch: one captured step per vector count (index n - 1;
+    // null where capture failed: that count launches from the stream)
+    std::vector<hipGraphExec_t> gexec_n;
     std::mutex mu;
 };
 
@@ -1694,6 +1697,23 @@ int build_model(cmolhip_model *m, const cmolhip_model_desc_t *d, const Plan &P)
             HC(ce);
             HC(hipGraphInstantiate(&B.gexec, B.graph, nullptr, nullptr, 0));
         }
+        // the shared batch: every per-step input (tokens, positions, cache
+        // slots) lives in device buffers, so one capture per vector count
+        // replays any step of that size
+        Batch &M = *m->multi;
+        M.gexec_n.assign(M.cap, nullptr);
+        for (int n = 1; n <= M.cap; n++) {
+            hipGraph_t gr = nullptr;
+            if (hipStreamBeginCapture(M.st, hipStreamCaptureModeThreadLocal) != hipSuccess) break;
+            const int rc = enqueue_step(m, M, n, M.st);
+            const hipError_t ce = hipStreamEndCapture(M.st, &gr);
+            if (rc == E_OK && ce == hipSuccess && gr) {
+                if (hipGraphInstantiate(&M.gexec_n[n - 1], gr, nullptr, nullptr, 0) != hipSuccess)
+                    M.gexec_n[n - 1] = nullptr;
+            }
+            if (gr) (void)hipGraphDestroy(gr);
+            (void)hipGetLastError();   // a failed capture leaves that count on stream launches
+        }
     }
     return E_OK;
 }
@@ -1703,6 +1723,17 @@ unsigned long long reduce_slots(const unsigned long long *k)
     unsigned long long best = 0;
     for (int i = 0; i < ARGMAX_SLOTS; i++) best = k[i] > best ? k[i] : best;
     return best;
+}
+
+// One step of the shared batch over its first n vectors: the captured
+// graph of that count, else stream launches.
+int run_multi(cmolhip_model *m, Batch &B, int n)
+{
+    if (n >= 1 && n <= (int)B.gexec_n.size() && B.gexec_n[n - 1]) {
+        HC(hipGraphLaunch(B.gexec_n[n - 1], B.st));
+        return E_OK;
+    }
+    return enqueue_step(m, B, n, B.st);
 }
 
 int run_single(cmolhip_model *m, Batch &B)
@@ -1735,6 +1766,8 @@ void destroy_batch(Batch &B)
 {
     if (B.st) (void)hipStreamSynchronize(B.st);
     if (B.gexec) (void)hipGraphExecDestroy(B.gexec);
+    for (hipGraphExec_t e : B.gexec_n)
+        if (e) (void)hipGraphExecDestroy(e);
     if (B.graph) (void)hipGraphDestroy(B.graph);
     if (B.st) (void)hipStreamDestroy(B.st);
     if (B.h_steps) (void)hipHostFree(B.h_steps);
@@ -1765,7 +1798,7 @@ int prompt_by_matvec(cmolhip_model_t *m, int slot, const int32_t *tokens, int n,
     }
     HC(hipMemcpyAsync(B.steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
     HC(hipMemcpyAsync(B.slot_ids, B.h_slots, (size_t)n * 4, hipMemcpyHostToDevice, B.st));
-    RC(enqueue_step(m, B, n, B.st));
+    RC(run_multi(m, B, n));
     const size_t V = m->hp.vocab;
     HC(hipMemcpyAsync(B.h_argmax, B.argmax + (size_t)(n - 1) * ARGMAX_SLOTS, ARGMAX_SLOTS * 8,
                       hipMemcpyDeviceToHost, B.st));
@@ -1979,7 +2012,7 @@ int decode_batch(cmolhip_model_t *m, int n, const int32_t *slots, const int32_t 
     }
     HC(hipMemcpyAsync(B.steps, B.h_steps, (size_t)n * 12, hipMemcpyHostToDevice, B.st));
     HC(hipMemcpyAsync(B.slot_ids, B.h_slots, (size_t)n * 4, hipMemcpyHostToDevice, B.st));
-    RC(enqueue_step(m, B, n, B.st));
+    RC(run_multi(m, B, n));
     return finish(m, B, n, logits_host, argmax, logits_each);
 }
 

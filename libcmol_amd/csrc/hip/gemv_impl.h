@@ -597,8 +597,11 @@ static inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 // measurements.
 static inline int gemv_lds_budget(int wgs)
 {
-    static const int kb = gb_env_int("CMOL_GEMV_LDS_KB", 0);
-    if (getenv("CMOL_GEMV_LDS_KB")) return kb * 1024;
+    static const int kb = [] {
+        const char *e = getenv("CMOL_GEMV_LDS_KB");
+        return e ? atoi(e) : 0;
+    }();
+    if (kb > 0) return kb * 1024;
     return wgs <= gemv_cus() ? 156 * 1024 : 80 * 1024;
 }
 
@@ -1119,9 +1122,12 @@ static int launch_gemv_b16_nw(const GemvArgs &a, const Gb16Shape &p, hipStream_t
 {
     constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
     const size_t lds = (size_t)p.sq * 4 * 2048 + 64;
-    static const bool lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI, NWB>,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                   160 * 1024) == hipSuccess;
+    // set once; a refusal (e.g. inside a stream capture) is retried on the
+    // next launch rather than remembered
+    static bool lds_ok = false;
+    if (!lds_ok)
+        lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI, NWB>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     if (!lds_ok) return -6;
     const long blocks = (long)((p.rblocks * p.splits + 7) / 8) * 8 * p.groups;
     const bool split = p.splits > 1;
