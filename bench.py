@@ -359,14 +359,75 @@ def copy_calibration(mb, reps=4):
     return {"copy_bytes": nbytes, "copies": reps}
 
 
+def cgroup_cpu_quota():
+    """CPUs the process's cgroup allows (cpu.max quota / period; cgroup v1's
+    cfs files), or None when unlimited or unreadable."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+            return None if q == "max" else int(q) / int(per)
+    except (OSError, ValueError):
+        pass
+    try:
+        with open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us") as f:
+            q = int(f.read())
+        with open("/sys/fs/cgroup/cpu/cpu.cfs_period_us") as f:
+            per = int(f.read())
+        return None if q <= 0 else q / per
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_cores():
-    """Host threads the CPU baselines use: the CPU share of one GPU (at most
-    16, and at most what OMP_NUM_THREADS allows)."""
-    n = os.cpu_count() or 1
+    """Host threads the CPU baselines use: the CPUs this process may run on
+    (its affinity mask and its cgroup's quota), at most OMP_NUM_THREADS and
+    at most 16 (the CPU share of one GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    q = cgroup_cpu_quota()
+    if q is not None:
+        n = min(n, max(1, int(q)))
     e = os.environ.get("OMP_NUM_THREADS", "")
     if e.isdigit() and int(e) > 0:
         n = min(n, int(e))
     return max(1, min(n, 16))
+
+
+ISA_FLAGS = ("sse4_2", "avx", "avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512dq",
+             "avx512_vnni", "avx512_bf16", "avx512_fp16", "amx_tile")
+
+
+def oracle_build_flags():
+    """The oracle's compiler flags, read from oracle/Makefile (OFLAGS)."""
+    try:
+        with open(os.path.join(ROOT, "oracle", "Makefile")) as f:
+            for line in f:
+                if line.startswith("OFLAGS"):
+                    return "gcc " + line.split("=", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def host_cpu():
+    """The host the CPU baselines ran on: CPU model, logical CPUs, the CPUs
+    this process may use (affinity, cgroup quota) and the x86 ISA extensions
+    /proc/cpuinfo reports."""
+    model, flags = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "model name" and model is None:
+                    model = v.strip()
+                elif k == "flags" and not flags:
+                    flags = set(v.split())
+    except OSError:
+        pass
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": aff,
+            "cgroup_cpu_quota": cgroup_cpu_quota(),
+            "isa": [f for f in ISA_FLAGS if f in flags], "oracle_build": oracle_build_flags()}
 
 
 def cpu_baseline(cores, c4_tokens=3):
@@ -416,6 +477,22 @@ def cpu_baseline(cores, c4_tokens=3):
     out["c1_decode_1"] = {"value": 32 / el, "unit": "tok/s", "cores": 1,
                           "effective_weight_GBps": round(wb1 * 32 / el / 1e9, 2),
                           "sample": "32 decode steps after a 32-token prompt"}
+    # C1 through the reference itself (built from its own sources), when it
+    # travelled with the tree: its runtime-selected AVX-512 / AVX2 kernels
+    if O.ref_available():
+        rm = O.RefModel(synth.model_file(spec1), max_ctx=72)
+        for p in range(32):
+            rm.forward(int(toks[p]), p)
+        t0 = time.perf_counter()
+        for p in range(32, 64):
+            rm.forward(int(toks[p]), p)
+        el = time.perf_counter() - t0
+        rm.close()
+        out["c1_decode_1_reference"] = {
+            "value": 32 / el, "unit": "tok/s", "cores": 1, "kind": "reference",
+            "kernel": O.ref().shim_kernel_name().decode(),
+            "effective_weight_GBps": round(wb1 * 32 / el / 1e9, 2),
+            "sample": "32 decode steps after a 32-token prompt, the reference's cmol_model_forward"}
     # C3: SmolLM2-360M-shaped Q5_0, 16 sessions at uniform lengths 64..1024
     spec_3 = synth.PRESETS["smollm2-360m-q5_0"]
     lens = synth.uniform_lengths(16, 64, 1024, seed=5).astype(int)
@@ -447,7 +524,9 @@ def cpu_baseline(cores, c4_tokens=3):
     head = out["c4_decode_1"]
     return {"value": round(head["value"], 4), "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": "SmolLM3-3B-shaped Q4_0 single session, " + head["sample"]
-                      + "; the oracle in the reference's AVX-512 accumulation order",
+                      + "; the oracle in the reference's AVX-512 accumulation order (the reference "
+                        "has no Q4_0 kernel, so no reference figure exists for this model)",
+            "threads_available": cores, "host": host_cpu(),
             "configs": out}
 
 
@@ -456,10 +535,40 @@ TRAFFIC_SHAPE = (11008, 2048)
 
 
 def traffic_child():
-    """Run under rocprofv3 by measure_traffic: a device-to-device copy of known
-    size (the calibration kernel), then the roofline matvec."""
+    """Run under rocprofv3 by measure_traffic and trace_pass: a device-to-device
+    copy of known size (the counters' calibration kernel), then the roofline
+    matvec exactly as the matvec leg times it (64 rotating weight copies,
+    8 untimed + 256 event-timed launches)."""
     copy_calibration(64, reps=4)
-    bench_matvec(TRAFFIC_SHAPE[0], TRAFFIC_SHAPE[1], 1, copies=32, launches=32)
+    r = bench_matvec(TRAFFIC_SHAPE[0], TRAFFIC_SHAPE[1], 1, copies=64, launches=256)
+    print(json.dumps(r), flush=True)
+
+
+def trace_pass(workdir):
+    """One rocprofv3 kernel-trace pass over traffic_child: mean, min and max
+    duration (us) of the roofline matvec's dispatches, from the trace's own
+    start and end timestamps, and the event-timed figure of the same run."""
+    env = dict(os.environ, TMPDIR="/tmp")
+    cmd = ["timeout", "-s", "KILL", "180", "rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv",
+           "-d", workdir, "-o", "trace", "--", sys.executable, os.path.join(ROOT, "bench.py"), "--traffic-child"]
+    res = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.DEVNULL,
+                         check=True, text=True)
+    ev = None
+    for line in res.stdout.splitlines():
+        if line.startswith("{"):
+            ev = json.loads(line)
+    path = None
+    for root, _, files in os.walk(workdir):
+        for f in files:
+            if f.startswith("trace") and f.endswith("kernel_trace.csv"):
+                path = os.path.join(root, f)
+    durs = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Kernel_Name"].startswith("void k_gemv<"):
+                durs.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return {"calls": len(durs), "avg_us": sum(durs) / len(durs), "min_us": min(durs), "max_us": max(durs),
+            "event_us": ev["us_per_launch"] if ev else None}
 
 
 def pmc_pass(counter, workdir):
@@ -488,23 +597,33 @@ def pmc_pass(counter, workdir):
 
 
 def measure_traffic():
-    """HBM bytes per launch of the roofline matvec: FETCH_SIZE and WRITE_SIZE
-    (two passes), each scaled by what it reads for the 64 MiB copy.  None when
-    rocprofv3 is unavailable or a pass fails."""
+    """The roofline matvec measured by rocprofv3 in this run: a kernel-trace
+    pass (its dispatch durations) and HBM bytes per launch from FETCH_SIZE and
+    WRITE_SIZE (two counter passes), each scaled by what it reads for the
+    64 MiB copy.  Parts whose pass failed, or all of it without rocprofv3,
+    are None."""
     if not shutil.which("rocprofv3"):
-        return None
+        return None, None
+    errs = (subprocess.CalledProcessError, OSError, KeyError, ValueError, ZeroDivisionError, TypeError)
     work = tempfile.mkdtemp(prefix="cmol_pmc_", dir="/tmp")
+    trace = traffic = None
     try:
-        cf, mf = pmc_pass("FETCH_SIZE", work)
-        cw, mw = pmc_pass("WRITE_SIZE", work)
-    except (subprocess.CalledProcessError, OSError, KeyError, ValueError, ZeroDivisionError, TypeError):
-        return None
+        try:
+            trace = trace_pass(os.path.join(work, "trace"))
+        except errs:
+            trace = None
+        try:
+            cf, mf = pmc_pass("FETCH_SIZE", work)
+            cw, mw = pmc_pass("WRITE_SIZE", work)
+            copy_kib = 64 * 1024
+            fs, ws = copy_kib / cf, copy_kib / cw
+            traffic = {"bytes": int((mf * fs + mw * ws) * 1024), "fetch_KiB": round(mf, 1),
+                       "write_KiB": round(mw, 1), "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
+        except errs:
+            traffic = None
     finally:
         shutil.rmtree(work, ignore_errors=True)
-    copy_kib = 64 * 1024
-    fs, ws = copy_kib / cf, copy_kib / cw
-    return {"bytes": int((mf * fs + mw * ws) * 1024), "fetch_KiB": round(mf, 1), "write_KiB": round(mw, 1),
-            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
+    return trace, traffic
 
 
 def main():
@@ -597,11 +716,11 @@ def main():
         log("32 concurrent cmol_generate callers")
         g32 = bench_generate_concurrent(path, spec, args.sessions, args.generate_tokens)
         log(json.dumps(g32))
-    traffic = None
+    traffic = trace = None
     if mv and "traffic" not in skip:
-        log("roofline kernel traffic (two rocprofv3 counter passes)")
-        traffic = measure_traffic()
-        log(json.dumps(traffic))
+        log("roofline kernel under rocprofv3 (a kernel-trace pass, then two counter passes)")
+        trace, traffic = measure_traffic()
+        log(json.dumps({"trace": trace, "traffic": traffic}))
     cpu = None
     if "cpu" not in skip:
         log("cpu baseline")
@@ -611,16 +730,27 @@ def main():
     weight_bytes = spec.weight_bytes_per_token()
     roof = None
     if mv:
+        # achieved / frac from the rocprofv3 kernel trace of this run (the
+        # profiler's dispatch durations), else from the HIP events
         r = mv[0]
-        roof = {"bound": "hbm", "achieved": round(r["GBps"], 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(r["frac_of_peak"], 4),
+        b = r["bytes_per_launch"]
+        us = trace["avg_us"] if trace else r["us_per_launch"]
+        roof = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBPS, 4),
                 "traffic": traffic["bytes"] if traffic else recorded_traffic("gemv_q4_11008x2048_traffic.txt"),
                 "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes in this run, scaled by a 64 MiB "
                                    "copy: " + json.dumps(traffic)) if traffic else
                                   "profiles/gemv_q4_11008x2048_traffic.txt (no counter pass in this run)",
                 "kernel": "k_gemv<Q4_0> 11008x2048 n=1",
-                "bytes_per_launch": r["bytes_per_launch"],
-                "us_per_launch": round(r["us_per_launch"], 3)}
+                "bytes_per_launch": b,
+                "us_per_launch": round(us, 3),
+                "us_source": ("rocprofv3 --kernel-trace pass in this run: mean of the dispatches' end - start "
+                              "over the rotating-copy launches" if trace else
+                              "HIP events (no kernel-trace pass in this run)"),
+                "trace": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in trace.items()}
+                if trace else None,
+                "us_per_launch_events": round(r["us_per_launch"], 3),
+                "frac_events": round(r["frac_of_peak"], 4)}
     if d1 is None:
         print(json.dumps({"metric": METRIC, "matvec": mv, "gemm": gm, "roofline": roof, "decode_135m_1": c1,
                           "decode_360m_16": c3, "decode_32": d32, "cpu_baseline": cpu}), flush=True)

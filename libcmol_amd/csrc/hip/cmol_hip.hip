@@ -1038,6 +1038,8 @@ struct cmolhip_model {
     float *pk_ex = nullptr;       // exchange buffers of both parities
     size_t pk_ex_n = 0;           // floats at pk_ex
     int *h_pk_err = nullptr;      // pinned copy of pk.err
+    unsigned pk_launches = 0;     // persistent launches since the last reset (exchange set = parity)
+    int pk_giveups = 0;           // steps the graph redid after a persistent wait gave up
     unsigned long long *h_trace = nullptr;   // pinned copy of the last step's stage times
     int trace_n = 0;
 };
@@ -1458,8 +1460,8 @@ int launch_persist(int dt, const PkArgs &a, int nwg, int lds, hipStream_t s)
 // gave up).
 int persist_reset(cmolhip_model *m, hipStream_t st)
 {
+    m->pk_launches = 0;   // the next launch uses exchange set 0
     HC(hipMemsetD32Async((hipDeviceptr_t)m->pk_ex, (int)PK_POISON, m->pk_ex_n, st));
-    HC(hipMemsetAsync(m->pk.tok, 0, 4, st));
     HC(hipMemsetAsync(m->pk.err, 0, 4, st));
     return E_OK;
 }
@@ -1548,7 +1550,6 @@ int build_persist(cmolhip_model *m, int dt)
     a.max_splits = ms;
     a.op_bytes = opb;
     a.eps = h.rms_eps;
-    RC(cmolhip_alloc(c, 4, ALIGN, (void **)&a.tok));
     RC(cmolhip_alloc(c, 4, ALIGN, (void **)&a.err));
     RC(persist_reset(m, c->stream));
     HC(hipHostMalloc((void **)&m->h_pk_err, 4, hipHostMallocDefault));
@@ -1579,11 +1580,16 @@ int build_persist(cmolhip_model *m, int dt)
     return E_OK;
 }
 
+// Steps whose persistent wait gave up before the model stays on the graph.
+constexpr int PK_GIVEUP_MAX = 4;
+
 // One decode step of the single session with the persistent kernel (the
 // step record is already on its way to B.steps on B.st).
 int run_persist(cmolhip_model *m, Batch &B)
 {
     PkArgs a = m->pk;
+    a.par = (int)(m->pk_launches & 1u);   // launches are serialised by the session's lock
+    m->pk_launches++;
     a.step = B.steps;
     a.slot_id = B.slot_ids;
     a.logits = B.logits;
@@ -1896,7 +1902,12 @@ int cmolhip_decode(cmolhip_model_t *m, int slot, int32_t token, int32_t pos, flo
     if (m->pk_dt) {
         RC(run_persist(m, B));
         RC(finish(m, B, 1, logits_host, argmax));
-        return persist_check(m, B);
+        const int rc = persist_check(m, B);
+        if (rc != E_UNSUPPORTED) return rc;
+        // a wait gave up (a slow or contended step): the decode graph redoes
+        // the step from the record already in B.steps (it rewrites the same
+        // cache row); after PK_GIVEUP_MAX such steps the model stays on the graph
+        if (++m->pk_giveups >= PK_GIVEUP_MAX) m->pk_dt = 0;
     }
     RC(run_single(m, B));
     return finish(m, B, 1, logits_host, argmax);

@@ -7,6 +7,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <atomic>
 #include <cstdlib>
 
 // k-split finish of the batched matvec (gemv.hip): sums the `splits`
@@ -357,9 +358,14 @@ void k_gemv(GemvArgs a, GemvShape sh)
         const int qd = quad_of(i);
         q_load<DT>(a.w, cell0 + qd, l & 15, l, c0[u], c1[u], dv[u], hv[u]);
         if constexpr (DIRECT) {
+            // padding blocks of the last quad (k/32 not a multiple of 4) have
+            // no operand rows: they re-read the last real block's, so the
+            // product with their zero scale is 0, whatever stale bytes lie
+            // past the operand
 #pragma unroll
             for (int bi = 0; bi < 4; bi++)
-                xo[u][bi] = ldg((const f16x8 *)((const uint8_t *)a.in.q + (uint32_t)(4 * qd + bi) * (uint32_t)vb + xoff));
+                xo[u][bi] = ldg((const f16x8 *)((const uint8_t *)a.in.q +
+                                                (uint32_t)min(4 * qd + bi, nblk - 1) * (uint32_t)vb + xoff));
         }
     };
 #pragma unroll
@@ -1123,12 +1129,15 @@ static int launch_gemv_b16_nw(const GemvArgs &a, const Gb16Shape &p, hipStream_t
     constexpr int U = (DT == DT_Q8_0) ? 6 : 8;
     const size_t lds = (size_t)p.sq * 4 * 2048 + 64;
     // set once; a refusal (e.g. inside a stream capture) is retried on the
-    // next launch rather than remembered
-    static bool lds_ok = false;
-    if (!lds_ok)
-        lds_ok = hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI, NWB>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-    if (!lds_ok) return -6;
+    // next launch rather than remembered (decode threads of several sessions
+    // may get here at once: the flag is atomic, the attribute call idempotent)
+    static std::atomic<bool> lds_ok{false};
+    if (!lds_ok.load(std::memory_order_relaxed)) {
+        if (hipFuncSetAttribute((const void *)k_gemv_b16<DT, U, EPI, NWB>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return -6;
+        lds_ok.store(true, std::memory_order_relaxed);
+    }
     const long blocks = (long)((p.rblocks * p.splits + 7) / 8) * 8 * p.groups;
     const bool split = p.splits > 1;
     if (a.ev_start)

@@ -361,7 +361,7 @@ struct PkArgs {
     int d, n_heads, n_kv, d_head, d_ffn, max_ctx, kv_f16, max_splits;
     int op_bytes;                  // LDS operand area (largest matrix operand + zero slot)
     float eps;
-    unsigned *tok;                 // launches so far: this launch's parity is *tok & 1
+    int par;                       // this launch's exchange-buffer set: launches since the last reset, mod 2
     int *err;                      // set when a wait gave up (the step's outputs are invalid)
     unsigned long long *trace;     // optional: work-group 0's stage times
     unsigned long long *marks;     // optional: [stage][work-group][PK_MARKS] phase times

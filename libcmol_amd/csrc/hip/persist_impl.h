@@ -1137,8 +1137,7 @@ __global__ __launch_bounds__(PK_THREADS) void k_persist(PkArgs a)
     // per-launch values, uniform across the work-group (scalar registers:
     // the addresses built from them stay scalar)
     PkSt S;
-    S.par = __builtin_amdgcn_readfirstlane(
-        (int)(__hip_atomic_load(a.tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1u));
+    S.par = a.par & 1;
     S.tok = __builtin_amdgcn_readfirstlane(a.step[0]);
     S.pos = min(max(__builtin_amdgcn_readfirstlane(a.step[1]), 0), a.max_ctx - 1);
     S.L = min(max(__builtin_amdgcn_readfirstlane(a.step[2]), 1), a.max_ctx);
@@ -1189,14 +1188,8 @@ __global__ __launch_bounds__(PK_THREADS) void k_persist(PkArgs a)
         pk_mark(a, pk_stages(a.n_layers) - 1, 2);
     }
 
-    // the launch counter moves on (work-group 0, last: every work-group read
-    // it at its start, before any of work-group 0's waits could complete)
     pk_mark(a, pk_stages(a.n_layers) - 1, 6);
     if (a.trace && wg == 0 && tid == 0) a.trace[1] = wall_clock64();
-    if (wg == 0 && tid == 0) {
-        __builtin_amdgcn_s_waitcnt(0);
-        __hip_atomic_fetch_add(a.tok, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
 }
 
 // Launches k_persist for layer format DL (cooperative: all work-groups

@@ -109,6 +109,37 @@ def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
 
 
 @pytest.mark.parametrize("dtype,rows,cols,fold,n", [
+    (2, 2048, 11040, 1, 8), (8, 160, 8288, 1, 8), (6, 100, 11008 + 32, 1, 5)])
+def test_gemv_direct_padding_ignores_stale_operand(ctx, dtype, rows, cols, fold, n):
+    """The operand read straight from L2 (beyond the LDS budget, at most one
+    work-group per CU) with k/32 not a multiple of 4: the last quad's
+    padding blocks have no operand rows, and the buffer past the last real
+    block holds f16 NaN before the operand is prepared.  The result must not
+    see them."""
+    import ctypes as C
+    import libcmol_amd.native as native
+    raw = random_blocks(dtype, rows, cols, seed=rows + 9 * cols + n)
+    x = np.random.default_rng(n + 3).standard_normal((n, cols)).astype(np.float32)
+    t = ctx.qtensor([raw], dtype, cols, [rows], fold=fold)
+    L = native.lib()
+    nbytes = L.cmolhip_act_bytes(cols, n)
+    quads = (cols // 32 + 3) // 4
+    op = ctx.alloc(quads * 4 * 128 * n + 4096)   # room for whole quads, stale NaN throughout
+    ctx.h2d(op, np.full((quads * 4 * 128 * n + 4096) // 2, 0x7E00, np.uint16))
+    assert nbytes <= quads * 4 * 128 * n + 4096
+    dx = ctx.upload(x)
+    native.check(L.cmolhip_act_prepare(ctx.h, C.c_void_p(dx), n, cols, dtype, None, C.c_void_p(op), None),
+                 "act_prepare")
+    dy = ctx.alloc(n * rows * 4)
+    ctx.gemm_prepared(t, op, n, None, dy)
+    native.check(L.cmolhip_synchronize(ctx.h), "sync")
+    got = ctx.d2h(dy, (n, rows), np.float32)
+    want = O.matmul(raw, np.ascontiguousarray(x.T), rows, cols, dtype, O.AVX512).T
+    assert np.isfinite(got).all(), "padding blocks read stale NaN operand bytes"
+    assert_close(got, want, f"direct gemv q{dtype} {rows}x{cols} n {n}")
+
+
+@pytest.mark.parametrize("dtype,rows,cols,fold,n", [
     (2, 384, 2048, 1, 33), (2, 256, 2048, 1, 64), (2, 300, 2048, 1, 130), (8, 576, 576, 1, 200),
     (6, 320, 960, 1, 97), (6, 2560, 960, 1, 64), (2, 2048, 11008, 4, 65), (2, 3072, 2048, 4, 128),
     (8, 200, 576, 8, 70), (6, 960, 960, 2, 96), (2, 37, 4096, 1, 40), (2, 512, 2048, 1, 512),

@@ -69,3 +69,26 @@ def test_noalloc_refuses_oversized_scratch(ctx):
     assert rc == 0
     want = ctx.gemm(t, x2)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_noalloc_direct_padding_after_nan_call(ctx):
+    """A call whose operand ends in f16 NaN (11136 inputs, NaN in the last
+    96), then one of 11040 inputs at the same vector count: the second reads
+    its operand straight from L2, and the padding blocks of its last quad sit
+    where the first call left NaN in the scratch.  Its result must equal
+    cmolhip_gemm's bit for bit."""
+    rng = np.random.default_rng(21)
+    raw0 = random_blocks(2, 2048, 11136, seed=31)
+    t0 = ctx.qtensor([raw0], 2, 11136, [2048])
+    x0 = rng.standard_normal((8, 11136)).astype(np.float32)
+    x0[:, -96:] = np.nan
+    rc, _ = noalloc(ctx, t0, x0, None)
+    assert rc == 0
+    raw = random_blocks(2, 2048, 11040, seed=32)
+    t = ctx.qtensor([raw], 2, 11040, [2048])
+    x = rng.standard_normal((8, 11040)).astype(np.float32)
+    want = ctx.gemm(t, x)
+    rc, got = noalloc(ctx, t, x, None)
+    assert rc == 0
+    assert np.isfinite(got).all()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
