@@ -34,10 +34,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
 //   * online softmax over the 64 scores with wave reductions;
 //   * weighted sum with lanes over the dimensions: each position's weight is
 //     broadcast with readlane and its V row read once per wave.
+// With NWV = 8 waves and at most four query heads per kv head, two waves
+// serve each head, each on one half of every chunk's positions (their
+// online softmaxes meet at the end of the split), so each wave's dependent
+// chains are half as long and two waves share a SIMD; with more heads wave
+// w serves head w alone.
 // Same partial format as attn_split, merged by k_attn_merge.
 #define ATH_CH 64
-template <int DH, typename KT, int CH>
-__global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
+template <int DH, typename KT, int CH, int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
 {
 #pragma clang fp contract(off)
     constexpr int RB = DH * (int)sizeof(KT);        // row bytes
@@ -45,12 +50,15 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     constexpr int PE = 16 / (int)sizeof(KT);         // elements per 16-byte piece
     constexpr int NPL = RB / 16 / 4;                 // pieces per lane (a quarter of the row)
     constexpr int DL = DH / 64;                      // output dims per lane
+    constexpr int NT = NWV * 64;
     constexpr int UNITS = CH * RB / 16;              // 16-byte units of a chunk's K (and of V)
-    constexpr int UPT = UNITS / 256;                 // per thread
+    constexpr int UPT = UNITS / NT;                  // per thread
     constexpr int PS = CH / 16;                      // 16-position passes per chunk
-    static_assert(UNITS % 256 == 0 && CH % 16 == 0, "chunk size");
+    static_assert(UNITS % NT == 0 && CH % 16 == 0, "chunk size");
+    static_assert(NWV == 4 || (NWV == 8 && PS % 2 == 0), "waves");
     __shared__ __attribute__((aligned(16))) uint8_t ks[2][CH * KS];
     __shared__ __attribute__((aligned(16))) uint8_t vs[2][CH * RB];
+    __shared__ float xm[4], xl[4], xo[4][DH];        // NWV = 8: the second halves' results
 
     const int kvh = blockIdx.x, sp = blockIdx.y, n = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -66,13 +74,13 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     const uint8_t *kb = (const uint8_t *)((const KT *)a.kv.k_base + off);
     const uint8_t *vb = (const uint8_t *)((const KT *)a.kv.v_base + off);
 
-    // staging: thread tid moves units tid + 256u of K and V (rows past the
+    // staging: thread tid moves units tid + NT u of K and V (rows past the
     // split re-read its last row; their weights are zero)
     u32x4 kr[UPT], vr[UPT];
     auto fetch = [&](int c) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
-            const int unit = tid + 256 * u, row = unit / (RB / 16), col = unit % (RB / 16);
+            const int unit = tid + NT * u, row = unit / (RB / 16), col = unit % (RB / 16);
             const size_t src = (size_t)min(c * CH + row, cnt - 1) * RB + col * 16;
             kr[u] = ldg((const u32x4 *)(kb + src));
             vr[u] = ldg((const u32x4 *)(vb + src));
@@ -81,15 +89,20 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
     auto put = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
-            const int unit = tid + 256 * u, row = unit / (RB / 16), col = unit % (RB / 16);
+            const int unit = tid + NT * u, row = unit / (RB / 16), col = unit % (RB / 16);
             *(u32x4 *)&ks[buf][row * KS + col * 16] = kr[u];
             *(u32x4 *)&vs[buf][row * RB + col * 16] = vr[u];
         }
     };
 
     // queries of this wave's heads: lane quarter j holds pieces j, j+4, ...
+    // (NWV = 8: head hw, passes ps0 .. ps0 + PSW - 1 of each chunk)
     const int j = lane & 3;
-    const int nh = wid < G ? (wid + 4 < G ? 2 : 1) : 0;
+    constexpr bool PAIRS = NWV == 8;
+    constexpr int PSW = PAIRS ? PS / 2 : PS;
+    const int hw = PAIRS ? (wid & 3) : wid, half = PAIRS ? (wid >> 2) : 0;
+    const int ps0 = half * PSW;
+    const int nh = PAIRS ? (hw < G ? 1 : 0) : (wid < G ? (wid + 4 < G ? 2 : 1) : 0);
     float q[2][NPL * PE];
     float m[2], l[2], o[2][DL];
 #pragma unroll
@@ -98,7 +111,7 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
         l[hh] = 0.0f;
 #pragma unroll
         for (int d = 0; d < DL; d++) o[hh][d] = 0.0f;
-        const int g = min(wid + 4 * hh, G - 1);
+        const int g = min(PAIRS ? hw : wid + 4 * hh, G - 1);
         const float *qh = a.q + (size_t)n * a.q_stride + (size_t)(kvh * G + g) * DH;
 #pragma unroll
         for (int i = 0; i < NPL; i++)
@@ -118,9 +131,10 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
         for (int hh = 0; hh < 2; hh++) {
             if (hh >= nh) break;
             // scores: pass ps covers positions 16 ps + lane/4
-            float sc[PS];
+            float sc[PSW];
 #pragma unroll
-            for (int ps = 0; ps < PS; ps++) {
+            for (int pw = 0; pw < PSW; pw++) {
+                const int ps = ps0 + pw;
                 const uint8_t *kr0 = &ks[buf][(16 * ps + (lane >> 2)) * KS];
                 float dot = 0.0f;
 #pragma unroll
@@ -141,18 +155,21 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
                 }
                 dot += __shfl_xor(dot, 1, 64);
                 dot += __shfl_xor(dot, 2, 64);
-                sc[ps] = (16 * ps + (lane >> 2)) < np ? dot * scale : -INFINITY;
+                sc[pw] = (16 * ps + (lane >> 2)) < np ? dot * scale : -INFINITY;
             }
             float mc = sc[0];
 #pragma unroll
-            for (int ps = 1; ps < PS; ps++) mc = fmaxf(mc, sc[ps]);
+            for (int pw = 1; pw < PSW; pw++) mc = fmaxf(mc, sc[pw]);
             mc = wave_max(mc);
             const float mn = fmaxf(m[hh], mc);
-            float ev[PS], ls = 0.0f;
+            // a half-chunk wave may not have met a valid position yet
+            // (uniform over the wave)
+            if (PAIRS && mn == -INFINITY) continue;
+            float ev[PSW], ls = 0.0f;
 #pragma unroll
-            for (int ps = 0; ps < PS; ps++) {
-                ev[ps] = expf(sc[ps] - mn);
-                if (j == 0) ls += ev[ps];
+            for (int pw = 0; pw < PSW; pw++) {
+                ev[pw] = expf(sc[pw] - mn);
+                if (j == 0) ls += ev[pw];
             }
             ls = wave_sum(ls);
             const float al = expf(m[hh] - mn);
@@ -162,10 +179,11 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
             for (int d = 0; d < DL; d++) o[hh][d] *= al;
             // weighted sum: lane covers dims DL*lane ..
 #pragma unroll
-            for (int ps = 0; ps < PS; ps++) {
+            for (int pw = 0; pw < PSW; pw++) {
+                const int ps = ps0 + pw;
 #pragma unroll 4
                 for (int r = 0; r < 16; r++) {
-                    const float ep = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[ps]), 4 * r));
+                    const float ep = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[pw]), 4 * r));
                     const uint8_t *vrow = &vs[buf][(16 * ps + r) * RB];
                     if constexpr (sizeof(KT) == 4) {
                         if constexpr (DL == 2) {
@@ -194,13 +212,36 @@ __global__ __launch_bounds__(256) void k_attn_h(AttnArgs a)
         }
     }
 
+    // NWV = 8: the second halves hand their (m, l, o) to the first, which
+    // combine them with the log-sum-exp rule
+    if constexpr (PAIRS) {
+        if (half == 1 && nh) {
+#pragma unroll
+            for (int d = 0; d < DL; d++) xo[hw][DL * lane + d] = o[0][d];
+            if (lane == 0) {
+                xm[hw] = m[0];
+                xl[hw] = l[0];
+            }
+        }
+        __syncthreads();
+        if (half == 1) return;
+        if (nh) {
+            const float m1 = xm[hw], M = fmaxf(m[0], m1);
+            const float a0 = m[0] == -INFINITY ? 0.0f : expf(m[0] - M);
+            const float a1 = m1 == -INFINITY ? 0.0f : expf(m1 - M);
+            l[0] = l[0] * a0 + xl[hw] * a1;
+            m[0] = M;
+#pragma unroll
+            for (int d = 0; d < DL; d++) o[0][d] = o[0][d] * a0 + xo[hw][DL * lane + d] * a1;
+        }
+    }
     // partials (or the finished output when the session fits one split)
     const bool single = nact == 1;
     const size_t sbase = (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         if (hh >= nh) break;
-        const int g = wid + 4 * hh;
+        const int g = PAIRS ? hw : wid + 4 * hh;
 #pragma unroll
         for (int d = 0; d < DL; d++) {
             const int dim = DL * lane + d;
@@ -636,18 +677,29 @@ int launch_attn(const AttnArgs &a, hipStream_t s)
 #define ATT(DHV)                                                                          \
     if (a.kv_f16) hipLaunchKernelGGL((k_attn<DHV, _Float16>), grid, block, 0, s, a);      \
     else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);
-#define ATH(DHV)                                                                                  \
-    if (half_chunks) {                                                                            \
-        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, 32>), grid, block, 0, s, a);    \
-        else hipLaunchKernelGGL((k_attn_h<DHV, float, 32>), grid, block, 0, s, a);               \
-    } else {                                                                                      \
-        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, ATH_CH>), grid, block, 0, s, a); \
-        else hipLaunchKernelGGL((k_attn_h<DHV, float, ATH_CH>), grid, block, 0, s, a);           \
+#define ATH(DHV)                                                                                      \
+    if (half_chunks) {                                                                                \
+        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, 32, 4>), grid, block, 0, s, a);     \
+        else hipLaunchKernelGGL((k_attn_h<DHV, float, 32, 4>), grid, block, 0, s, a);                \
+    } else if (h8) {                                                                                  \
+        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, ATH_CH, 8>), grid, block8, 0, s, a); \
+        else hipLaunchKernelGGL((k_attn_h<DHV, float, ATH_CH, 8>), grid, block8, 0, s, a);           \
+    } else {                                                                                          \
+        if (a.kv_f16) hipLaunchKernelGGL((k_attn_h<DHV, _Float16, ATH_CH, 4>), grid, block, 0, s, a); \
+        else hipLaunchKernelGGL((k_attn_h<DHV, float, ATH_CH, 4>), grid, block, 0, s, a);            \
     }
     // head-per-wave kernel for short splits (one or two chunks); the
     // thread-per-dimension kernel streams long splits better
     const char *e = getenv("CMOL_ATTN_H");
     const bool head_waves = half_chunks || (e ? e[0] == '1' : a.split <= 2 * ATH_CH);
+    // eight waves (two per query head) when the kv head has at most four
+    // query heads (CMOL_ATTN_H8=0: four waves, measurements)
+    static const bool h8_on = [] {
+        const char *v = getenv("CMOL_ATTN_H8");
+        return !(v && v[0] == '0');
+    }();
+    const bool h8 = h8_on && G <= 4;
+    const dim3 block8(512);
     switch (a.d_head) {
     case 16: ATT(16); break;
     case 32: ATT(32); break;

@@ -480,7 +480,7 @@ template <int DH, int NT, typename M>
 __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n)
 {
     constexpr int SG = NT / DH;
-    constexpr int MP = 16;   // o values per thread loaded with the (m, l)
+    constexpr int MP = 24;   // o values per thread loaded with the (m, l) (48 splits at d_head 128)
     const int tid = threadIdx.x;
     const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
     const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
