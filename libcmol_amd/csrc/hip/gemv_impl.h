@@ -21,6 +21,7 @@ struct GemvShape {
     int op_bytes;   // LDS bytes of the operand area (staged blocks + zero slot)
     int zslot;      // LDS byte offset of the 16 zero bytes unused operand rows read
     int ss_bytes;   // LDS bytes of the sum-of-squares partials
+    int groups = 1; // vector groups of 8 (grid.y): more than 8 vectors run as n = 8 per work-group
 };
 
 template <typename M = StPlain>
@@ -48,6 +49,21 @@ __device__ inline void stage_dma(const void *src, uint8_t *dst, int bytes, int w
         if (off < bytes)
             __builtin_amdgcn_global_load_lds((const gvoid_t *)((const uint8_t *)src + off),
                                              (lvoid_t *)(dst + k * 1024), 16, 0, 0);
+    }
+}
+
+// The operand rows of vectors v0 .. v0 + nv - 1 (nv <= 8) of an nb-vector
+// operand, gathered into LDS in the 8-vector layout: block k takes 1 KiB,
+// [4 k-groups][16 rows][16 B]; lane l copies row l % 16 of k-group l / 16
+// (rows past the group re-read its last row: their products are discarded).
+template <int NW>
+__device__ inline void stage_dma_group(const void *src, uint8_t *dst, int nblk, int nb, int v0, int nv, int wid,
+                                       int l)
+{
+    const int r = 2 * v0 + min(l & 15, 2 * nv - 1);
+    for (int k = wid; k < nblk; k += NW) {
+        const uint8_t *p = (const uint8_t *)src + (((size_t)k * 4 + (l >> 4)) * 2 * nb + r) * 16;
+        __builtin_amdgcn_global_load_lds((const gvoid_t *)p, (lvoid_t *)(dst + (size_t)k * 1024), 16, 0, 0);
     }
 }
 
@@ -310,14 +326,20 @@ void k_gemv(GemvArgs a, GemvShape sh)
     uint8_t *s_op = smem;
     float *s_ss = (float *)(smem + sh.op_bytes);
     float *s_nrm = (float *)(smem + sh.op_bytes + sh.ss_bytes);
-    float *s_z = s_nrm + ((a.n + 3) & ~3);
+    // vector group (grid.y > 1, more than 8 vectors): the work-group serves
+    // vectors v0 .. v0 + n - 1 of the batch, its operand rows gathered into
+    // the 8-vector LDS layout (nl vectors)
+    const bool grouped = gridDim.y > 1;
+    const int v0 = grouped ? (int)blockIdx.y * 8 : 0;
+    const int nl = grouped ? 8 : a.n;
+    float *s_z = s_nrm + ((nl + 3) & ~3);
 
     // fold F = 2^lf (1..8) parts of R = 16/F = 2^lr rows per tile
     const int BQ = a.w.block_quads, F = a.w.fold, lf = __builtin_ctz(F), lr = 4 - lf, R = 1 << lr;
     const int t = blockIdx.x;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
-    const int n = a.n;
-    const int vb = 128 * n;              // operand bytes per block
+    const int n = grouped ? min(8, a.n - v0) : a.n;   // this work-group's vectors
+    const int vb = 128 * nl;             // operand bytes per block in LDS
     const int nblk = a.w.cols >> 5;
     const int qpc = sh.qpc, cq = NW * qpc;
     const int nchunks = CHUNKED ? (BQ + cq - 1) / cq : 1;
@@ -330,11 +352,15 @@ void k_gemv(GemvArgs a, GemvShape sh)
     const int pv = (int)threadIdx.x >> lr, prow = t * R + ((int)threadIdx.x & (R - 1));
     const bool pact = pre_on && (int)threadIdx.x < n * R && prow < a.w.rows;
     EpiPre pre;
-    epi_pre_load(a, epi, pv, prow, pact, pre);
+    epi_pre_load(a, epi, v0 + pv, prow, pact, pre);
 
     // ---- 1. operand and norm partials into LDS (issued first) ----
-    if constexpr (!CHUNKED && !DIRECT) stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
-    if (a.in.ss) stage_ss_dma<NW>(a.in.ss, a.in.ss_stride, a.in.ss_count, n, s_ss, wid, l);
+    if constexpr (!CHUNKED && !DIRECT) {
+        if (grouped) stage_dma_group<NW>(a.in.q, s_op, nblk, a.n, v0, n, wid, l);
+        else stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
+    }
+    if (a.in.ss)
+        stage_ss_dma<NW>(a.in.ss + (size_t)v0 * a.in.ss_stride, a.in.ss_stride, a.in.ss_count, n, s_ss, wid, l);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. weight ring: slot u holds sequence element i with i % U == u;
@@ -348,7 +374,9 @@ void k_gemv(GemvArgs a, GemvShape sh)
     // layout a staged copy would have; A rows past the batch re-read the
     // last vector's row (their outputs are discarded)
     f16x8 xo[DIRECT ? U : 1][4];
-    const uint32_t xoff = DIRECT ? (uint32_t)(((l >> 4) * 2 * n + min(l & 15, 2 * n - 1)) * 16) : 0u;
+    // (global layout of the whole batch: a.n vectors; a group's rows start at 2 v0)
+    const uint32_t vbg = 128u * (uint32_t)a.n;
+    const uint32_t xoff = DIRECT ? (uint32_t)(((l >> 4) * 2 * a.n + 2 * v0 + min(l & 15, 2 * n - 1)) * 16) : 0u;
     auto quad_of = [&](int i) {
         i = min(i, len - 1);
         const int c = CHUNKED ? i / qpc : 0;
@@ -365,7 +393,7 @@ void k_gemv(GemvArgs a, GemvShape sh)
 #pragma unroll
             for (int bi = 0; bi < 4; bi++)
                 xo[u][bi] = ldg((const f16x8 *)((const uint8_t *)a.in.q +
-                                                (uint32_t)min(4 * qd + bi, nblk - 1) * (uint32_t)vb + xoff));
+                                                (uint32_t)min(4 * qd + bi, nblk - 1) * vbg + xoff));
         }
     };
 #pragma unroll
@@ -398,7 +426,7 @@ void k_gemv(GemvArgs a, GemvShape sh)
         const int v = ar >> (lf + 1), p = (ar >> 1) & (F - 1), h = ar & 1;
         const bool ok = v < n;
         const int p0 = CHUNKED ? 0 : p * 4 * BQ;
-        abase[gi] = ok ? p0 * vb + (g * 2 * n + 2 * v + h) * 16 : sh.zslot;
+        abase[gi] = ok ? p0 * vb + (g * 2 * nl + 2 * v + h) * 16 : sh.zslot;
         astride[gi] = ok ? vb : 0;
     }
 
@@ -539,15 +567,16 @@ void k_gemv(GemvArgs a, GemvShape sh)
         }
         float y = z * ACT_INV_SCALE;
         if (EPI != EPI_RESID && a.in.ss) y *= s_nrm[v];
+        const int gv = v0 + v;   // the vector's index in the batch
         if constexpr (EPI >= 0) {
-            epilogue<EPI >= 0 ? EPI : 0>(a, t, rl, R, v, act, y, pre_on, pre);
+            epilogue<EPI >= 0 ? EPI : 0>(a, t, rl, R, gv, act, y, pre_on, pre);
         } else {
             switch (sh.epi) {
-            case EPI_STORE: epilogue<EPI_STORE>(a, t, rl, R, v, act, y); break;
-            case EPI_RESID: epilogue<EPI_RESID>(a, t, rl, R, v, act, y, pre_on, pre); break;
-            case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, rl, R, v, act, y); break;
-            case EPI_QKV: epilogue<EPI_QKV>(a, t, rl, R, v, act, y, pre_on, pre); break;
-            default: epilogue<EPI_LOGITS>(a, t, rl, R, v, act, y); break;
+            case EPI_STORE: epilogue<EPI_STORE>(a, t, rl, R, gv, act, y); break;
+            case EPI_RESID: epilogue<EPI_RESID>(a, t, rl, R, gv, act, y, pre_on, pre); break;
+            case EPI_SWIGLU: epilogue<EPI_SWIGLU>(a, t, rl, R, gv, act, y); break;
+            case EPI_QKV: epilogue<EPI_QKV>(a, t, rl, R, gv, act, y, pre_on, pre); break;
+            default: epilogue<EPI_LOGITS>(a, t, rl, R, gv, act, y); break;
             }
         }
     }
@@ -614,21 +643,23 @@ static inline int gemv_lds_budget(int wgs)
 // Chooses quads per wave per chunk and the LDS areas; returns the dynamic
 // LDS bytes or -1 when the operand cannot be staged (`chunked` is set when
 // it takes more than one chunk, only possible with fold 1).
-static inline int plan_gemv(const GemvArgs &a, int nw, GemvShape &sh, bool &chunked)
+static inline int plan_gemv(const GemvArgs &a, int nw, GemvShape &sh, bool &chunked, int groups = 1)
 {
     const int BQ = a.w.block_quads, F = a.w.fold;
-    const int vb = 128 * a.n;
-    sh.ss_bytes = a.in.ss ? round_up(a.n * a.in.ss_count * 4, 16) : 0;
-    const int nrm = round_up(a.n * 4, 16);
-    const int red = nw * a.n * 64;   // per-wave useful entries (16 columns x n floats)
-    const int cap = gemv_lds_budget(a.w.row_tiles) - sh.ss_bytes - nrm - red - 16;
+    const int n = groups > 1 ? 8 : a.n;   // vectors per work-group
+    sh.groups = groups;
+    const int vb = 128 * n;
+    sh.ss_bytes = a.in.ss ? round_up(n * a.in.ss_count * 4, 16) : 0;
+    const int nrm = round_up(n * 4, 16);
+    const int red = nw * n * 64;   // per-wave useful entries (16 columns x n floats)
+    const int cap = gemv_lds_budget(a.w.row_tiles * groups) - sh.ss_bytes - nrm - red - 16;
     const long full = (long)F * 4 * BQ * vb;
     if (full <= cap) {
         chunked = false;
         sh.qpc = (BQ + nw - 1) / nw;
         sh.zslot = (int)full;
     } else {
-        if (F != 1) return -1;
+        if (F != 1 || groups > 1) return -1;
         chunked = true;
         sh.qpc = cap / (4 * vb * nw);
         if (sh.qpc < 1) return -1;
@@ -648,7 +679,7 @@ struct GemvRing {
 template <typename K>
 static void gemv_go(K kern, const GemvArgs &a, const GemvShape &sh, int lds, int nw, hipStream_t s)
 {
-    const dim3 grid(a.w.row_tiles), block(nw * 64);
+    const dim3 grid(a.w.row_tiles, sh.groups), block(nw * 64);
     // a refused attribute skips the launch; launch_gemv reports it
     // through hipGetLastError
     if (lds > 64 * 1024 &&
@@ -689,14 +720,14 @@ int launch_gemv_epi(const GemvArgs &a, const GemvShape &sh, int lds, int len, hi
 #endif
 
 template <int DT, int NW, int NG>
-static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
+static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s, int groups = 1)
 {
     if (epi < EPI_STORE || epi > EPI_LOGITS) return -6;
     GemvShape sh;
     sh.epi = epi;
     bool chunked = false;
-    const int lds = plan_gemv(a, NW, sh, chunked);
-    if (lds < 0) return -6;
+    const int lds = plan_gemv(a, NW, sh, chunked, groups);
+    if (lds < 0 || (groups > 1 && (NG != 1 || a.w.fold != 1 || chunked))) return -6;
     using RG = GemvRing<DT>;
     // an operand beyond the budget on a grid of at most one work-group per
     // CU: each wave reads its own quads' operand from L2 in its weight ring
@@ -736,23 +767,23 @@ static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s)
 
 // Widest wave count the launch heuristics allow whose LDS plan fits.
 template <int DT, int NG>
-static int launch_dt(const GemvArgs &a, int epi, hipStream_t s)
+static int launch_dt(const GemvArgs &a, int epi, hipStream_t s, int groups = 1)
 {
-    int nw = pick_nw(a.w.row_tiles, a.w.block_quads, DT == DT_Q4_0 && NG == 1);
+    int nw = pick_nw(a.w.row_tiles * groups, a.w.block_quads, DT == DT_Q4_0 && NG == 1);
     for (;; nw >>= 1) {
         GemvShape sh;
         bool ch;
-        if (nw <= 1 || plan_gemv(a, nw, sh, ch) >= 0) break;
+        if (nw <= 1 || plan_gemv(a, nw, sh, ch, groups) >= 0) break;
     }
     // 16 waves leave 128 VGPRs a lane: only the single-group Q4_0 kernel
     // fits without spilling
     if constexpr (NG == 1 && DT == DT_Q4_0) {
-        if (nw >= 16) return launch_cfg<DT, 16, NG>(a, epi, s);
+        if (nw >= 16) return launch_cfg<DT, 16, NG>(a, epi, s, groups);
     }
-    if (nw >= 8) return launch_cfg<DT, 8, NG>(a, epi, s);
-    if (nw >= 4) return launch_cfg<DT, 4, NG>(a, epi, s);
-    if (nw >= 2) return launch_cfg<DT, 2, NG>(a, epi, s);
-    return launch_cfg<DT, 1, NG>(a, epi, s);
+    if (nw >= 8) return launch_cfg<DT, 8, NG>(a, epi, s, groups);
+    if (nw >= 4) return launch_cfg<DT, 4, NG>(a, epi, s, groups);
+    if (nw >= 2) return launch_cfg<DT, 2, NG>(a, epi, s, groups);
+    return launch_cfg<DT, 1, NG>(a, epi, s, groups);
 }
 
 // ---------------------------------------------------------------------------
@@ -1208,9 +1239,36 @@ static int launch_gemv_b(const GemvArgs &a, int epi, hipStream_t s)
     return 0;
 }
 
+// 9..32 vectors as groups of 8 on grid.y of the one-group matvec (waves
+// split k inside the work-group, the epilogue runs in place): taken where the
+// batched kernel would split k across work-groups (a finish kernel after it)
+// and the 8-vector operand fits LDS whole.  CMOL_GEMV_GROUPS=0 turns it off
+// (measurements).
+template <int DT>
+static bool gemv_grouped(const GemvArgs &a)
+{
+    static const bool on = [] {
+        const char *e = getenv("CMOL_GEMV_GROUPS");
+        return !(e && e[0] == '0');
+    }();
+    if (!on || is_kquant(DT) || a.w.fold != 1 || a.n <= GB_VG || a.n > 32) return false;
+    GbShape sh;
+    gb_plan(a.w, a.n, sh);
+    Gb16Shape p;
+    const int splits = gb16_plan(a.w, a.n, p) ? p.splits : sh.splits;
+    if (splits <= 1) return false;
+    const int groups = (a.n + GB_VG - 1) / GB_VG;
+    GemvShape gs;
+    bool ch = false;
+    for (int nw = 16; nw >= 2; nw >>= 1)
+        if (plan_gemv(a, nw, gs, ch, groups) >= 0 && !ch) return true;
+    return false;
+}
+
 template <int DT>
 int launch_ng(const GemvArgs &a, int epi, hipStream_t s)
 {
+    if (gemv_grouped<DT>(a)) return launch_dt<DT, 1>(a, epi, s, (a.n + GB_VG - 1) / GB_VG);
     if (gemv_batched(a.w, a.n)) return launch_gemv_b<DT>(a, epi, s);
     const int rows = 2 * a.n * a.w.fold;   // MFMA A rows
     if (rows <= 16) return launch_dt<DT, 1>(a, epi, s);
