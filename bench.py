@@ -752,8 +752,9 @@ def main():
                 "us_per_launch_events": round(r["us_per_launch"], 3),
                 "frac_events": round(r["frac_of_peak"], 4)}
     if d1 is None:
-        print(json.dumps({"metric": METRIC, "matvec": mv, "gemm": gm, "roofline": roof, "decode_135m_1": c1,
-                          "decode_360m_16": c3, "decode_32": d32, "cpu_baseline": cpu}), flush=True)
+        print(json.dumps({"metric": METRIC, "matvec": mv, "gemm": gm, "roofline": roof, "sampled_1": s1,
+                          "decode_135m_1": c1, "decode_360m_16": c3, "decode_32": d32, "generate_32": g32,
+                          "cpu_baseline": cpu}), flush=True)
         return
     ctx1 = d1["context"] + args.warmup + args.steps / 2
     with_roofline(d1, weight_bytes + kv_bytes(spec, ctx1, 4))

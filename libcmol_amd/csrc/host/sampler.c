@@ -16,10 +16,15 @@
 #ifndef _DEFAULT_SOURCE
 #define _DEFAULT_SOURCE
 #endif
+#ifndef _GNU_SOURCE
+#define _GNU_SOURCE   /* sched_getaffinity, CPU_COUNT */
+#endif
 #include "internal.h"
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
@@ -197,13 +202,37 @@ static void *pool_worker(void *arg)
     }
 }
 
+/* CPUs the process may use: the online CPUs, bounded by its affinity mask
+ * and by its cgroup's CPU quota (cgroup v2 cpu.max). */
+static long usable_cpus(void)
+{
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    cpu_set_t set;
+    if (sched_getaffinity(0, sizeof set, &set) == 0) {
+        const long c = CPU_COUNT(&set);
+        if (c > 0 && c < n) n = c;
+    }
+    FILE *f = fopen("/sys/fs/cgroup/cpu.max", "r");
+    if (f) {
+        char q[32];
+        long per = 0;
+        if (fscanf(f, "%31s %ld", q, &per) == 2 && strcmp(q, "max") != 0 && per > 0) {
+            long c = atol(q) / per;
+            if (c < 1) c = 1;
+            if (c < n) n = c;
+        }
+        fclose(f);
+    }
+    return n < 1 ? 1 : n;
+}
+
 /* Worker count: cmol__sampler_config's, else CMOL_SAMPLER_THREADS, else half
- * the online CPUs, at most 8. */
+ * the CPUs the process may use, at most 8. */
 static int pool_size(void)
 {
     if (pool_threads_wanted >= 0) return pool_threads_wanted;
     const char *e = getenv("CMOL_SAMPLER_THREADS");
-    long n = e ? atol(e) : sysconf(_SC_NPROCESSORS_ONLN) / 2;
+    long n = e ? atol(e) : usable_cpus() / 2;
     if (!e && n > 8) n = 8;
     if (n < 0) n = 0;
     if (n > POOL_MAX) n = POOL_MAX;
