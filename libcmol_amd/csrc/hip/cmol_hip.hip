@@ -376,7 +376,7 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
     // the arena space of k-split partial sums is released at once: later
     // work on this stream runs after the kernels
     const size_t mark = arena_mark(c);
-    const size_t pf = n <= 32 ? gemv_part_floats(to_qt(*w), n) : 0;
+    const size_t pf = n <= 32 ? gemv_part_floats(to_qt(*w), n) : gemm_part_floats(to_qt(*w), n);
     float *part = nullptr;
     int rc = pf ? arena_get(c, pf, &part) : E_OK;
     if (rc == E_OK) rc = launch_product(c, w, op, n, ss, eps, dy, part, pf, ev_start, ev_stop);
@@ -413,7 +413,7 @@ int cmolhip_gemm_noalloc(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const flo
     // scratch layout: operand | sum-of-squares partials | k-split partial sums
     const size_t op_b = align_up(act_bytes(w->cols, n), ALIGN);
     const size_t ss_b = norm_w ? align_up((size_t)n * (w->cols / 32) * 4, ALIGN) : 0;
-    const size_t pf = n <= 32 ? gemv_part_floats(to_qt(*w), n) : 0;
+    const size_t pf = n <= 32 ? gemv_part_floats(to_qt(*w), n) : gemm_part_floats(to_qt(*w), n);
     if (op_b + ss_b + pf * 4 > NOALLOC_SCRATCH_BYTES) return E_ARGS;   // beyond the fixed scratch
     float *ss = norm_w ? (float *)(base + op_b) : nullptr;
     float *part = pf ? (float *)(base + op_b + ss_b) : nullptr;
@@ -562,6 +562,8 @@ struct Prefill {
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
     float *qkv_raw = nullptr;                 // QK-norm models: [cap][d + 2 kvd]
     _Float16 *kv_hl = nullptr;                // prompt attention: high/low f16 copy of one layer's cache
+    float *part = nullptr;                    // split-K partial sums of the prompt GEMMs
+    size_t part_cap = 0;                      // floats at part
     int32_t *h_steps = nullptr;               // pinned [cap][3]
     int32_t *h_slots = nullptr;               // pinned [cap]
     std::mutex mu;
@@ -897,6 +899,14 @@ void plan_batch(Plan &P, const cmolhip_model_desc_t *d, int cap, int ms)
     if (has_qk_norm(d)) P.add((size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head) * 4);
 }
 
+// Partial sums a prompt pass's split-K GEMMs may need: GEMM_KS_MAX ranges of
+// the pass's tokens for the widest of q|k|v and the d_model-row matrices.
+size_t prefill_part_floats(const cmolhip_hparams_t &h)
+{
+    const size_t rows = (size_t)h.d_model + 2 * (size_t)h.n_kv_heads * h.d_head;
+    return (size_t)GEMM_KS_MAX * prefill_cap(h) * rows;
+}
+
 // Buffers of the prompt pass, in allocation order (mirrored by build_prefill).
 void plan_prefill(Plan &P, const cmolhip_model_desc_t *d)
 {
@@ -920,6 +930,7 @@ void plan_prefill(Plan &P, const cmolhip_model_desc_t *d)
     P.add((size_t)cap * np * h.d_head * 4);
     if (has_qk_norm(d)) P.add((size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head) * 4);
     if (prompt_attn_fits(h)) P.add(attn_prompt_kv_bytes(h.n_kv_heads, h.d_head, h.max_ctx));
+    P.add(prefill_part_floats(h) * 4);
 }
 
 
@@ -1273,6 +1284,8 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         g.kv = kv;
         g.pos = F.steps + 1;
         g.pos_stride = 3;
+        g.part = F.part;
+        g.part_cap = F.part_cap;
         if (L.q_norm || L.k_norm) {
             RC(enqueue_qk_norm(m, L, g, F.qkv_raw, kv, n, st, true));
         } else {
@@ -1316,6 +1329,8 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         go.out_stride = d;
         go.n = n;
         go.next = act_out(F.op_gu, L.gu.dtype, n, L.ffn_norm, F.ss_b, P);
+        go.part = F.part;
+        go.part_cap = F.part_cap;
         RC(launch_gemm(go, EPI_RESID, st));
 
         GemvArgs gu{};
@@ -1324,6 +1339,8 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
         gu.out = nullptr;
         gu.n = n;
         gu.next = act_out(F.op_dn, L.down.dtype, n, nullptr, nullptr, 0);
+        gu.part = F.part;
+        gu.part_cap = F.part_cap;
         RC(launch_gemm(gu, EPI_SWIGLU, st));
 
         GemvArgs gd{};
@@ -1336,6 +1353,8 @@ int enqueue_prefill(cmolhip_model *m, Prefill &F, Batch &B, int n, bool last, hi
             gd.next = act_out(F.op_qkv, m->layers[l + 1].qkv[0].dtype, n, m->layers[l + 1].attn_norm, F.ss_a, P);
         else
             gd.next = act_out(F.op_lm, lm_tensor(m).dtype, n, m->out_norm, F.ss_a, P);
+        gd.part = F.part;
+        gd.part_cap = F.part_cap;
         RC(launch_gemm(gd, EPI_RESID, st));
         ss_count = tile_count;
     }
@@ -1430,6 +1449,8 @@ int build_prefill(cmolhip_model *m, Prefill &F)
     if (m->qk_norm) RC(arena_get(c, (size_t)cap * (h.d_model + 2 * h.n_kv_heads * h.d_head), &F.qkv_raw));
     if (prompt_attn_fits(h))
         RC(arena_get(c, attn_prompt_kv_bytes(h.n_kv_heads, h.d_head, h.max_ctx) / sizeof(_Float16), &F.kv_hl));
+    F.part_cap = prefill_part_floats(h);
+    RC(arena_get(c, F.part_cap, &F.part));
     HC(hipHostMalloc((void **)&F.h_steps, (size_t)cap * 3 * 4, hipHostMallocDefault));
     HC(hipHostMalloc((void **)&F.h_slots, (size_t)cap * 4, hipHostMallocDefault));
     return E_OK;

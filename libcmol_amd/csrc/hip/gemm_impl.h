@@ -36,6 +36,7 @@ struct GemmShape {
     int vt;          // 16-row virtual tiles (ceil(rows / 16))
     int ga;          // XCD slices along the vector tiles (1, 2, 4, 8)
     int mts, nts;    // vector / row tiles per slice
+    int ks, kq;      // k ranges (grid.y) of kq block quads each; ks > 1: fp32 partial sums to a.part
 };
 
 // acc += the block's contribution for 16 vectors: xh holds their high
@@ -128,6 +129,8 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     const int BQ = a.w.block_quads, F = a.w.fold, R = 16 / F;
     const int nblk = a.w.cols >> 5;
     const int KQ = F * BQ;
+    // this work-group's k range (split-K over grid.y): quads kb .. ke - 1
+    const int kb = (int)blockIdx.y * sh.kq, ke = min(KQ, kb + sh.kq);
 
     // RMSNorm scales of the tile's vectors from the producer's partials,
     // passed through the last stage's LDS (untouched until the k loop's
@@ -180,7 +183,7 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     // every load is issued unconditionally (padding blocks re-read a valid
     // block) so the per-stage load count is fixed
     auto load_stage = [&](int st, int kk) {
-        kk = min(kk, KQ - 1);
+        kk = min(kk, ke - 1);
         const int p = kk / BQ, q = kk - p * BQ;
         const int b0 = p * 4 * BQ + 4 * q;
 #pragma unroll
@@ -211,7 +214,7 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
         const int p = kk / BQ, q = kk - p * BQ;
         // blocks of this quad: padding blocks of the last part and the steps
         // past the end of the k range contribute nothing
-        const int nb = kk < KQ ? min(4, nblk - (p * 4 * BQ + 4 * q)) : 0;
+        const int nb = kk < ke ? min(4, nblk - (p * 4 * BQ + 4 * q)) : 0;
         const uint8_t *sa = s_a + st * ASTAGE;
         auto block = [&](int bi) {
             f16x8 wv[2], wl[2];
@@ -250,11 +253,11 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
     // outstanding; the wait and the barrier publish every wave's copy of kk
     // (and every wave is done with kk-1), then kk+1 is issued into the stage
     // kk-1 freed
-    load_stage(0, 0);
+    load_stage(0, kb);
     __builtin_amdgcn_sched_barrier(0);
     // the body is unconditional (steps past the end compute nothing and
     // re-read the last quad) so every wait count is the same on each pass
-    for (int k0 = 0; k0 < KQ; k0 += GEMM_STAGES) {
+    for (int k0 = kb; k0 < ke; k0 += GEMM_STAGES) {
 #pragma unroll
         for (int u = 0; u < GEMM_STAGES; u++) {
             const int kk = k0 + u;
@@ -283,6 +286,13 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
                 const int v = m0 + vi;
                 const bool act = v < n;
                 float y = acc[h][j][e] * ACT_INV_SCALE;
+                if (sh.ks > 1) {
+                    // this k range's partial sum (the finish kernel adds the
+                    // ranges in order, then scales and runs the epilogue)
+                    const int row = V * 16 + cl;
+                    if (act && row < a.w.rows) a.part[((size_t)blockIdx.y * n + v) * a.w.rows + row] = y;
+                    continue;
+                }
                 if (a.in.ss) y *= nrm[h][e];
                 const int vv = act ? v : 0;
                 switch (sh.epi) {
@@ -297,11 +307,15 @@ __global__ __launch_bounds__(4 * WM * 64) void k_gemm(GemvArgs a, GemmShape sh)
 }
 
 template <int DT, int WM, int HG>
-int launch_gemm_wm(const GemvArgs &a, int epi, hipStream_t s)
+int launch_gemm_wm(const GemvArgs &a, int epi, hipStream_t s, int ks = 1)
 {
     constexpr int BM = 16 * HG * WM;
     GemmShape sh;
     sh.epi = epi;
+    const int KQ = a.w.fold * a.w.block_quads;
+    sh.ks = ks;
+    sh.kq = (KQ + ks - 1) / ks;
+    if (ks > 1 && (!a.part || (size_t)ks * a.n * a.w.rows > a.part_cap)) return -6;
     sh.mt = (a.n + BM - 1) / BM;
     sh.vt = (a.w.rows + 15) / 16;
     sh.nt = (sh.vt + 7) / 8;
@@ -314,12 +328,40 @@ int launch_gemm_wm(const GemvArgs &a, int epi, hipStream_t s)
     const long wgs = 8L * sh.mts * sh.nts;
     if (wgs > 0x7fffffffL) return -6;
     const size_t lds = (size_t)GEMM_STAGES * 4 * 4 * 2 * BM * 16;
+    const dim3 grid((unsigned)wgs, (unsigned)ks);
     if (a.ev_start)
-        hipExtLaunchKernelGGL((k_gemm<DT, WM, HG>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a.ev_start,
-                              a.ev_stop, 0, a, sh);
+        hipExtLaunchKernelGGL((k_gemm<DT, WM, HG>), grid, dim3(4 * WM * 64), lds, s, a.ev_start,
+                              ks > 1 ? nullptr : a.ev_stop, 0, a, sh);
     else
-        hipLaunchKernelGGL((k_gemm<DT, WM, HG>), dim3((unsigned)wgs), dim3(4 * WM * 64), lds, s, a, sh);
+        hipLaunchKernelGGL((k_gemm<DT, WM, HG>), grid, dim3(4 * WM * 64), lds, s, a, sh);
+    if (ks > 1) return launch_gemv_b_finish(a, epi, ks, a.in.ss ? a.in.ss_count : 0, s);
     return 0;
+}
+
+// k ranges of the split-K prompt GEMM: the fewest (a power of two, at most
+// GEMM_KS_MAX) that give the 64-vector tiles two work-groups per CU, each
+// range at least 8 block quads, within the partial-sum buffer; 1 when the
+// tiles already fill the chip or no buffer is given.  CMOL_GEMM_KSPLIT=0
+// turns it off (measurements).
+static inline int gemm_ks(const QTensor &w, int n, size_t part_cap)
+{
+    static const bool on = [] {
+        const char *e = getenv("CMOL_GEMM_KSPLIT");
+        return !(e && e[0] == '0');
+    }();
+    const long tiles64 = (long)((n + 63) / 64) * (((w.rows + 15) / 16 + 7) / 8);
+    const int KQ = w.fold * w.block_quads;
+    int ks = 1;
+    if (!on) return 1;
+    while (ks < GEMM_KS_MAX && tiles64 * ks < 2L * gemv_cus() && KQ / (2 * ks) >= 8 &&
+           (size_t)(2 * ks) * n * w.rows <= part_cap)
+        ks *= 2;
+    return ks;
+}
+
+static inline int gemm_ksplit(const GemvArgs &a, long)
+{
+    return a.part ? gemm_ks(a.w, a.n, a.part_cap) : 1;
 }
 
 // 64-vector work-groups (two per CU) unless their tiles cover at most half
@@ -336,6 +378,8 @@ int launch_gemm_dt(const GemvArgs &a, int epi, hipStream_t s)
     // the kernel's per-lane weight offsets are 32-bit
     if ((size_t)a.w.row_tiles * a.w.block_quads * 64 * QFmt<DT>::LANE_BYTES > 0xffffffffUL) return -6;
     const long tiles64 = (long)((a.n + 63) / 64) * (((a.w.rows + 15) / 16 + 7) / 8);
+    const int ks = gemm_ksplit(a, tiles64);
+    if (ks > 1) return launch_gemm_wm<DT, 2, 2>(a, epi, s, ks);
     if (tiles64 <= gemv_cus() / 2) return launch_gemm_wm<DT, 1, 2>(a, epi, s);
     return launch_gemm_wm<DT, 2, 2>(a, epi, s);
 }

@@ -21,7 +21,7 @@
 //            SwiGLU over interleaved gate/up rows [src/model.c:117-123];
 //            RoPE on q/k rows + KV-cache write at pos [src/attn.c:83-101];
 //            logits + first-index argmax [src/sampler.c:199-204].
-#include "gemv_impl.h"
+#include "gemm_impl.h"
 
 int launch_gemv_q4(const GemvArgs &a, int epi, hipStream_t s);
 int launch_gemv_q5(const GemvArgs &a, int epi, hipStream_t s);
@@ -71,6 +71,12 @@ int launch_gemm(const GemvArgs &a, int epi, hipStream_t s)
     }
     if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+size_t gemm_part_floats(const QTensor &w, int n)
+{
+    const int ks = gemm_ks(w, n, (size_t)-1);
+    return ks > 1 ? (size_t)ks * n * w.rows : 0;
 }
 
 size_t gemv_part_floats(const QTensor &w, int n)

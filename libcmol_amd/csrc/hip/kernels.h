@@ -246,9 +246,16 @@ int launch_gemv(const GemvArgs &a, int epi, hipStream_t s);
 // Scratch floats a batched (n > 8) matvec over w needs for its k-split
 // partial sums (0 when it does not split k).
 size_t gemv_part_floats(const QTensor &w, int n);
-// The same product for many vectors (prompt tokens): 64 x 64 output tiles,
-// epilogues EPI_STORE..EPI_QKV; any n >= 1.
+// Most k ranges a split-K prompt GEMM takes (its partial sums go to a.part).
+#define GEMM_KS_MAX 4
+// The same product for many vectors (prompt tokens): 64-vector x 128-row
+// output tiles, epilogues EPI_STORE..EPI_QKV; any n >= 1.  With a.part,
+// narrow matrices whose tiles would not fill the chip split k (fp32 partial
+// sums, then the k-split finish).
 int launch_gemm(const GemvArgs &a, int epi, hipStream_t s);
+// Partial-sum floats the split-K prompt GEMM of n vectors over w takes when
+// given room without limit (0 when it does not split).
+size_t gemm_part_floats(const QTensor &w, int n);
 // x [n][x_stride] fp32 -> operand (and sum-of-squares partials per 32 inputs).
 int launch_act_prep(const float *x, int x_stride, int K, int n, const ActOut &o, hipStream_t s);
 // Operand bytes for K inputs (padded to whole block quads) and n vectors.
