@@ -95,7 +95,12 @@ def test_gemv_matches_oracle(ctx, dtype, rows, cols, fold):
     # CU: read by the waves straight from L2 (partial row tiles included)
     (8, 160, 8192, 1, 8), (6, 100, 11008, 1, 5), (2, 70, 16384, 1, 7), (2, 2048, 11008, 1, 6),
     # more row tiles than CUs with such an operand: staged in chunks
-    (2, 4112, 11008, 1, 8), (8, 4100, 8192, 1, 3)])
+    (2, 4112, 11008, 1, 8), (8, 4100, 8192, 1, 3),
+    # 9-32 vectors where the batched plan would split k: groups of 8 on
+    # grid.y of the one-group kernel (full and ragged last groups; the 3B
+    # QKV / Wo and 360M QKV / down shapes)
+    (2, 3072, 2048, 1, 32), (2, 2048, 2048, 1, 32), (2, 2048, 2048, 1, 20), (2, 3072, 2048, 1, 27),
+    (6, 1600, 960, 1, 16), (6, 960, 2560, 1, 13), (8, 1000, 576, 1, 9)])
 def test_gemv_batched_matches_oracle(ctx, dtype, rows, cols, fold, n):
     """Several activation vectors per launch (multi-session decode), including
     operands staged in chunks or read from L2 (n * cols too large for one LDS
@@ -143,7 +148,10 @@ def test_gemv_direct_padding_ignores_stale_operand(ctx, dtype, rows, cols, fold,
     (2, 384, 2048, 1, 33), (2, 256, 2048, 1, 64), (2, 300, 2048, 1, 130), (8, 576, 576, 1, 200),
     (6, 320, 960, 1, 97), (6, 2560, 960, 1, 64), (2, 2048, 11008, 4, 65), (2, 3072, 2048, 4, 128),
     (8, 200, 576, 8, 70), (6, 960, 960, 2, 96), (2, 37, 4096, 1, 40), (2, 512, 2048, 1, 512),
-    (6, 1664, 960, 2, 640), (8, 2176, 576, 1, 600), (2, 2100, 2048, 4, 700)])
+    (6, 1664, 960, 2, 640), (8, 2176, 576, 1, 600), (2, 2100, 2048, 4, 700),
+    # split-K (tiles short of two work-groups per CU): the 3B down / Wo /
+    # QKV shapes at a 512-token pass, a ragged token tile, fold 2
+    (2, 2048, 11008, 1, 512), (2, 2048, 2048, 1, 512), (2, 3072, 2048, 1, 448), (2, 2048, 11008, 2, 300)])
 def test_gemm_tiled_matches_oracle(ctx, dtype, rows, cols, fold, n):
     """More than 32 vectors run the tiled MFMA GEMM (prompt prefill): partial
     row and vector tiles, folded weights read in place, and padding blocks.
@@ -158,18 +166,19 @@ def test_gemm_tiled_matches_oracle(ctx, dtype, rows, cols, fold, n):
     assert_close(got, want, f"tiled gemm q{dtype} {rows}x{cols} fold {fold} n {n}")
 
 
-def test_gemm_tiled_rmsnorm_prologue(ctx):
-    """The GEMM applies the RMSNorm scale from the operand's sums of squares."""
-    rows, cols, n = 256, 960, 80
-    raw = random_blocks(6, rows, cols, seed=9)
+@pytest.mark.parametrize("dtype,rows,cols,n", [(6, 256, 960, 80), (2, 2048, 2048, 200)])
+def test_gemm_tiled_rmsnorm_prologue(ctx, dtype, rows, cols, n):
+    """The GEMM applies the RMSNorm scale from the operand's sums of squares
+    (the second shape splits k: the finish kernel applies it)."""
+    raw = random_blocks(dtype, rows, cols, seed=9)
     rng = np.random.default_rng(11)
     x = (rng.standard_normal((n, cols)) * 3).astype(np.float32)
     w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
-    t = ctx.qtensor([raw], 6, cols, [rows])
+    t = ctx.qtensor([raw], dtype, cols, [rows])
     got = ctx.gemm(t, x, norm_w=w, eps=1e-6)
     xn = np.stack([O.rms_norm(xi, w, 1e-6) for xi in x])
-    want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, 6, O.AVX512).T
-    assert_close(got, want, "tiled gemm with rmsnorm")
+    want = O.matmul(raw, np.ascontiguousarray(xn.T), rows, cols, dtype, O.AVX512).T
+    assert_close(got, want, f"tiled gemm with rmsnorm {rows}x{cols} n {n}")
 
 
 @pytest.mark.parametrize("dtype,rows,cols,n", [
