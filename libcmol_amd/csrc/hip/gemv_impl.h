@@ -292,12 +292,13 @@ __device__ __forceinline__ void epilogue(const GemvArgs &a, int t, int rl, int R
 // without spilling and are held there (six waves per SIMD, six work-groups
 // per CU): pick_nw gives them matrices with more tiles than eight-wave
 // groups can keep resident at once.
-template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI, bool DIRECT = false>
+template <int DT, int NW, int NG, bool CHUNKED, int U, int EPI, bool DIRECT = false, bool GRP = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_0 && NW == 4 && NG == 1 && U == 4 && EPI != EPI_QKV && !DIRECT ? 6 : 1)))
 void k_gemv(GemvArgs a, GemvShape sh)
 {
     static_assert(!DIRECT || (NG == 1 && !CHUNKED), "direct operand: one group, no chunks");
+    static_assert(!GRP || (NG == 1 && !CHUNKED && !DIRECT), "vector groups: one operand group, staged whole");
     // launch arguments needed before the weight loads go out, fetched in
     // one round trip
     sgpr_pin(a.w.qs);
@@ -326,10 +327,11 @@ void k_gemv(GemvArgs a, GemvShape sh)
     uint8_t *s_op = smem;
     float *s_ss = (float *)(smem + sh.op_bytes);
     float *s_nrm = (float *)(smem + sh.op_bytes + sh.ss_bytes);
-    // vector group (grid.y > 1, more than 8 vectors): the work-group serves
-    // vectors v0 .. v0 + n - 1 of the batch, its operand rows gathered into
-    // the 8-vector LDS layout (nl vectors)
-    const bool grouped = gridDim.y > 1;
+    // vector group (GRP: grid.y runs over groups of 8 of more than 8
+    // vectors): the work-group serves vectors v0 .. v0 + n - 1 of the batch,
+    // its operand rows gathered into the 8-vector LDS layout (nl vectors);
+    // a compile-time switch, so the decode instances keep their code
+    constexpr bool grouped = GRP;
     const int v0 = grouped ? (int)blockIdx.y * 8 : 0;
     const int nl = grouped ? 8 : a.n;
     float *s_z = s_nrm + ((nl + 3) & ~3);
@@ -356,7 +358,7 @@ void k_gemv(GemvArgs a, GemvShape sh)
 
     // ---- 1. operand and norm partials into LDS (issued first) ----
     if constexpr (!CHUNKED && !DIRECT) {
-        if (grouped) stage_dma_group<NW>(a.in.q, s_op, nblk, a.n, v0, n, wid, l);
+        if constexpr (GRP) stage_dma_group<NW>(a.in.q, s_op, nblk, a.n, v0, n, wid, l);
         else stage_dma<NW>(a.in.q, s_op, nblk * vb, wid, l);
     }
     if (a.in.ss)
@@ -750,9 +752,16 @@ static int launch_cfg(const GemvArgs &a, int epi, hipStream_t s, int groups = 1)
         }
     }
     const int len = chunked ? ((a.w.block_quads + sh.qpc * NW - 1) / (sh.qpc * NW)) * sh.qpc : sh.qpc;
-    // the decode shape (one operand group, operand staged whole; residual
-    // epilogues take no RMSNorm there) runs the epilogue-specialised kernel
     if constexpr (NG == 1) {
+        // vector groups: the instance with the group gather, epilogue chosen
+        // at run time
+        if (groups > 1) {
+            if (len <= RG::S) gemv_go(k_gemv<DT, NW, 1, false, RG::S, -1, false, true>, a, sh, lds, NW, s);
+            else gemv_go(k_gemv<DT, NW, 1, false, RG::L, -1, false, true>, a, sh, lds, NW, s);
+            return 0;
+        }
+        // the decode shape (one operand group, operand staged whole; residual
+        // epilogues take no RMSNorm there) runs the epilogue-specialised kernel
         if (!chunked && !(epi == EPI_RESID && a.in.ss)) return launch_gemv_epi<DT, NW>(a, sh, lds, len, s);
     }
     if (chunked) {
