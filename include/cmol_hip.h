@@ -112,13 +112,15 @@ int cmolhip_gemm_prepared_timed(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, co
 /* No reference counterpart.  cmolhip_gemm for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * device allocation): the same product, computed by the same kernels, with
- * every piece of scratch (the activation operand, the RMSNorm partial sums
- * and the batched matvec's k-split partial sums) in one fixed device array
+ * every piece of scratch (the activation operand, the RMSNorm partial sums,
+ * the batched matvec's k-split partial sums and those of the split-K
+ * prompt GEMM for narrow matrices) in one fixed device array
  * of cmolhip_noalloc_scratch_bytes() bytes (16 MiB) per GPU, held from the
  * first cmolhip_ctx_create on that GPU until the process ends.  It calls no
  * allocator, host or device, and does not touch the context's arena.  A call
  * whose scratch would exceed the array (operand act_bytes(cols, n), plus
- * n*cols/32 floats with norm_w, plus the k-split sums of 9..32 vectors)
+ * n*cols/32 floats with norm_w, plus the k-split sums of 9..32 vectors or
+ * of the prompt GEMM's 2-4 k ranges: ranges x n x rows floats)
  * returns CMOL_ERR_ARGS without launching anything.  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (other threads or
  * other streams) race, so callers serialise them; each call writes all the
