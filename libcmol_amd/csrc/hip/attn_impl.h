@@ -277,7 +277,8 @@ __device__ __forceinline__ void attn_split(const AttnArgs &a, int kvh, int sp, i
 // weighted sum), so a chunk needs two barriers and 21 KB of LDS (d_head
 // 128).  Same partial format as attn_split.
 template <int DH, typename M>
-__device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp, int n)
+__device__ __forceinline__ void attn_piece_mf(const AttnArgs &a, int kvh, int n, int t0, int cnt, bool single,
+                                              size_t sbase)
 {
 #pragma clang fp contract(off)
     constexpr int NT = 256, CH = 64;
@@ -290,12 +291,7 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
     static_assert(DH >= 64 && DH % 64 == 0 && VPT >= 1, "shape");
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
     const int G = a.n_heads / a.n_kv;
-    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
-    const int t0 = sp * a.split;
-    if (t0 >= L) return;
-    const int cnt = min(L, t0 + a.split) - t0;
     const int nch = (cnt + CH - 1) / CH;
-    const int nact = (L + a.split - 1) / a.split;
 
     __shared__ float esh[ATT_MAX_G][CH];
     __shared__ __attribute__((aligned(16))) _Float16 ph[2][ATT_MAX_G][CH];
@@ -442,8 +438,6 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
 
     // outputs: lane l holds dimension d0 + 16t of heads 2(l/16) (rows 0, 1)
     // and 2(l/16) + 1 (rows 2, 3)
-    const bool single = nact == 1;
-    const size_t sbase = (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         const int h = 2 * g + k;
@@ -469,6 +463,307 @@ __device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp
     __syncthreads();   // the LDS areas may be reused by the caller
 }
 
+// The same piece with the four waves independent: wave w takes positions
+// 64j + 16w .. +15 of step j and keeps its own online softmax, so no
+// barrier stands between a wave's loads of one step and the next; the
+// waves meet once, at the end of the piece.
+//   * scores transposed, S^T = K . Q^T (16x16x32 f16): the cached K rows
+//     as stored are the A operand (row = position), the query's exact f16
+//     halves the B operand (column 2h / 2h+1 = high / low part of head h);
+//     lane l then holds positions 4(l/16) .. +3 of column l%16, the two
+//     parts of a head sit in neighbouring lanes, and the layout is already
+//     the A operand of the weighted sum (row = column, k = position);
+//   * lazy online softmax: a head's reference maximum m moves only when a
+//     score exceeds it by more than ATT_LAZY_T (a wave vote), so the common
+//     step needs no cross-lane reduction; weights e = exp(s - m) <= e^T stay
+//     exact f16 pairs (hi + lo/2048) and each lane sums its own e;
+//   * weighted sum P . V on 16x16x16 MFMAs: the wave's 16 V rows are staged
+//     in its own LDS rows (padded by four halves) and each B column (one
+//     dimension, four positions) is one transposing LDS read.
+// Same partial format as attn_split_mf; products exact, sums fp32.
+#define ATT_LAZY_T 8.0f
+template <int DH, typename M>
+__device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n, int t0, int cnt, bool single,
+                                               size_t sbase)
+{
+#pragma clang fp contract(off)
+    constexpr int NT = 256, NW = NT / 64;
+    constexpr int KS = DH / 32;           // score k-steps
+    constexpr int PPR = DH / 8;           // 16-byte pieces per cached row
+    constexpr int VPL = 16 * PPR / 64;    // V pieces per lane per step (16 rows)
+    constexpr int DT = DH / 16;           // 16-dimension output tiles
+    constexpr int RS = DH + 4;            // LDS row stride of the staged V (halves)
+    static_assert(DH >= 64 && DH % 64 == 0 && VPL >= 1, "shape");
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int col = lane & 15, grp = lane >> 4, part = col & 1;
+    const int G = a.n_heads / a.n_kv;
+    const int nst = (cnt + 63) / 64;
+
+    __shared__ __attribute__((aligned(16))) _Float16 vsw[NW][16 * RS];
+    // the end of the piece: each wave's (m, l, o) per head, over vsw
+    static_assert(NW * ATT_MAX_G * DH * 4 <= NW * 16 * RS * 2, "combine area");
+    __shared__ float xm[NW][ATT_MAX_G], xl[NW][ATT_MAX_G];
+    float *xo = (float *)vsw;
+
+    const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
+    const _Float16 *kb = (const _Float16 *)a.kv.k_base + off;
+    const _Float16 *vb = (const _Float16 *)a.kv.v_base + off;
+    f16x8 km[KS], vm[VPL];
+    auto load_k = [&](int j) {
+        const int p = min(64 * j + 16 * wid + col, cnt - 1);
+#pragma unroll
+        for (int s = 0; s < KS; s++) km[s] = ldg((const f16x8 *)(kb + (size_t)p * DH + 32 * s + 8 * grp));
+    };
+    // piece q = lane + 64i: row q / PPR of the step, dimensions 8 (q % PPR) .. +7
+    auto load_v = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++) {
+            const int q = lane + 64 * i;
+            const int p = min(64 * j + 16 * wid + q / PPR, cnt - 1);
+            vm[i] = ldg((const f16x8 *)(vb + (size_t)p * DH + 8 * (q % PPR)));
+        }
+    };
+    // B operand of the scores: lane l feeds column l%16 (head (l%16)/2, high
+    // or low part) with dimensions 32s + 8(l/16) .. +7 of k-step s, read
+    // straight from the query rows before the first K and V loads are
+    // issued (so waiting for them leaves those in flight)
+    const int rh = col >> 1;
+    const float *qh = a.q + (size_t)n * a.q_stride + (size_t)(kvh * G + (rh < G ? rh : 0)) * DH + 8 * grp;
+    float4 qv[KS][2];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        qv[s][0] = ldg((const float4 *)(qh + 32 * s));
+        qv[s][1] = ldg((const float4 *)(qh + 32 * s + 4));
+    }
+    load_k(0);
+    load_v(0);
+    const float scale = 1.0f / sqrtf((float)DH);
+    f16x8 qb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        const float xs[8] = {qv[s][0].x, qv[s][0].y, qv[s][0].z, qv[s][0].w,
+                             qv[s][1].x, qv[s][1].y, qv[s][1].z, qv[s][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float x = rh < G ? xs[e] : 0.0f;
+            const _Float16 hi = (_Float16)x;
+            qb[s][e] = part ? (_Float16)((x - (float)hi) * 2048.0f) : hi;
+        }
+    }
+    const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 oc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++) oc[t] = zero4;
+    float m = -INFINITY, lsum = 0.0f;   // head rh of this lane's column
+    _Float16 *vme = vsw[wid];
+
+    for (int j = 0; j < nst; j++) {
+        const int pb = 64 * j + 16 * wid;   // the wave's first position of the step
+        f32x4 sc = zero4;
+#pragma unroll
+        for (int s = 0; s < KS; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(km[s], qb[s], sc, 0, 0, 0);
+        if (j + 1 < nst) load_k(j + 1);
+        // the wave's 16 V rows into its LDS rows (8-byte writes)
+#pragma unroll
+        for (int i = 0; i < VPL; i++) {
+            const int q = lane + 64 * i;
+            uint64_t *w = (uint64_t *)(vme + (q / PPR) * RS + 8 * (q % PPR));
+            const u32x4 u = __builtin_bit_cast(u32x4, vm[i]);
+            w[0] = (uint64_t)u[0] | ((uint64_t)u[1] << 32);
+            w[1] = (uint64_t)u[2] | ((uint64_t)u[3] << 32);
+        }
+        if (j + 1 < nst) load_v(j + 1);
+        if (pb >= cnt) continue;   // every row of the wave past the piece (uniform)
+        // scores of positions pb + 4 grp + i: the high and low parts meet
+        // across the lane pair (l, l ^ 1)
+        float sv[4];
+        bool up = false;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float other = __int_as_float(
+                __builtin_amdgcn_mov_dpp(__float_as_int(sc[i]), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+            const float hi = part ? other : sc[i], lo = part ? sc[i] : other;
+            sv[i] = pb + 4 * grp + i < cnt ? (hi + lo * (1.0f / 2048.0f)) * scale : -INFINITY;
+            up |= sv[i] > m + ATT_LAZY_T;
+        }
+        if (__ballot(up)) {
+            // new reference maxima: the column's maximum over the 16 positions
+            float cm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+            cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+            const float mn = fmaxf(m, cm);
+            const float al = mn == m ? 1.0f : expf(m - mn);
+            m = mn;
+            lsum *= al;
+            // the output rows of this lane: heads 2 grp and 2 grp + 1, whose
+            // factors sit in the lanes of columns 4 grp and 4 grp + 2
+            const float a0 = __shfl(al, 4 * grp, 64), a1 = __shfl(al, 4 * grp + 2, 64);
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+                oc[t][0] *= a0;
+                oc[t][1] *= a0;
+                oc[t][2] *= a1;
+                oc[t][3] *= a1;
+            }
+        }
+        f16x4 pa;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float e = sv[i] > -INFINITY ? expf(sv[i] - m) : 0.0f;
+            lsum += e;
+            const _Float16 ehi = (_Float16)e;
+            pa[i] = part ? (_Float16)((e - (float)ehi) * 2048.0f) : ehi;
+        }
+        if (rh >= G) pa = f16x4{};
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            // B column: dimension 16t + col of positions 4 grp .. +3: within
+            // each 16-lane group, lane c reads dimensions 4(c%4) .. +3 of row
+            // 4 grp + c/4, and the read hands lane 4r+c element c of lanes 4e+r
+            const _Float16 *src = vme + (4 * grp + (col >> 2)) * RS + 16 * t + 4 * (col & 3);
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const s16x4 v4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)src);
+            oc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, v4), oc[t], 0, 0, 0);
+        }
+    }
+
+    // the waves meet: lane sums over the four row groups, then per head
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    __syncthreads();   // every wave done with its V rows: the area takes the outputs
+    if (grp == 0 && !part && rh < G) {
+        xm[wid][rh] = m;
+        xl[wid][rh] = lsum;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int h = 2 * grp + k;
+        if (h >= G) continue;
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+            xo[((size_t)wid * ATT_MAX_G + h) * DH + 16 * t + col] = oc[t][2 * k] + oc[t][2 * k + 1] * (1.0f / 2048.0f);
+    }
+    __syncthreads();
+    for (int i = tid; i < G * DH; i += NT) {
+        const int h = i / DH, d = i % DH;
+        float mx = xm[0][h];
+#pragma unroll
+        for (int w = 1; w < NW; w++) mx = fmaxf(mx, xm[w][h]);
+        float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = xm[w][h] > -INFINITY ? expf(xm[w][h] - mx) : 0.0f;
+            lt += xl[w][h] * f;
+            ot += xo[((size_t)w * ATT_MAX_G + h) * DH + d] * f;
+        }
+        if (single) {
+            const float fv = ot / lt;
+            const int kk = (kvh * G + h) * DH + d;
+            if (a.out) M::st(a.out + (size_t)n * a.out_stride + kk, fv);
+            if (a.next.q) act_put<M>(a.next, n, kk, fv);
+        } else {
+            M::st(a.po + (sbase + h) * DH + d, ot);
+            if (d == 0) {
+                M::st(a.pm + sbase + h, mx);
+                M::st(a.pl + sbase + h, lt);
+            }
+        }
+    }
+    __syncthreads();   // the LDS areas may be reused by the caller
+}
+
+// One split of attn_split's grid: positions sp*split .. of vector n; a
+// session that fits one split is finished here.
+template <int DH, typename M>
+__device__ __forceinline__ void attn_split_mf(const AttnArgs &a, int kvh, int sp, int n)
+{
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int t0 = sp * a.split;
+    if (t0 >= L) return;
+    const int G = a.n_heads / a.n_kv;
+    attn_piece_mf<DH, M>(a, kvh, n, t0, min(L, t0 + a.split) - t0, L <= a.split,
+                         (((size_t)n * a.n_kv + kvh) * a.max_splits + sp) * G);
+}
+
+// Balanced split (a.bal = B ranges per kv head).  The vectors' contexts are
+// laid end to end on one line, each preceded by ATT_BAL_PAD positions that
+// stand for the fixed cost of starting a piece (query load, pipeline fill);
+// range w of a kv head is the line's [wR, wR + R) with
+// R = max(split, ceil(line / B)), so the ranges hold about the same number
+// of cached rows whatever the mix of lengths.  The cut of vector n's
+// positions that falls in range w is a piece; pieces are in line order, so
+// slot w + n is unique to it, and vector n's pieces are the consecutive
+// slots w0 + n .. w1 + n.  Work-group k of a kv head (k < B + n_vectors)
+// runs the piece of slot k, if any, with attn_piece_mfw: the whole context
+// is finished here, a cut one written as the partial [kvh][k][G] that
+// k_attn_merge combines.
+// Unlike the split grid, no work-group starts only to find its split past
+// the context, and a long context leaves no tail of its own splits.
+#define ATT_BAL_PAD 64
+__device__ inline int wave_sum_i(int v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ inline int wave_scan_i(int v)   // inclusive prefix sum over the lanes
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+__device__ __forceinline__ int attn_len(const AttnArgs &a, int i)
+{
+    return i < a.n ? min(a.seqlen[i * a.seqlen_stride], a.max_ctx) : 0;
+}
+// Line length and range length of the balanced walk; every wave computes
+// them (no barrier), the attention and merge kernels alike.  l0: this
+// lane's context in the first 64 vectors.
+__device__ __forceinline__ int attn_bal_range(const AttnArgs &a, int l0)
+{
+    const int lane = threadIdx.x & 63;
+    int t = lane < a.n ? l0 + ATT_BAL_PAD : 0;
+    for (int b = 64; b < a.n; b += 64) t += b + lane < a.n ? attn_len(a, b + lane) + ATT_BAL_PAD : 0;
+    const int line = wave_sum_i(t);
+    return max(a.split, (line + a.bal - 1) / a.bal);
+}
+
+template <int DH, typename M>
+__device__ __forceinline__ void attn_bal_mf(const AttnArgs &a, int kvh, int k)
+{
+    const int lane = threadIdx.x & 63;
+    const int G = a.n_heads / a.n_kv;
+    const int l0 = attn_len(a, lane);
+    const int R = attn_bal_range(a, l0);
+    // the piece (w, s) with w + s = k: vector s's pieces are w0 .. w1
+    // (wave scans over blocks of 64 vectors; at most one lane matches)
+    int base = 0, s = -1, pj = 0, lj = 0;
+    for (int b = 0; b < a.n; b += 64) {
+        const int L = b == 0 ? l0 : attn_len(a, b + lane);
+        const int v = b + lane < a.n ? L + ATT_BAL_PAD : 0;
+        const int inc = wave_scan_i(v);
+        const int p0 = base + inc - v + ATT_BAL_PAD;   // line offset of the vector's position 0
+        const int w = k - (b + lane);
+        const uint64_t m = __ballot(b + lane < a.n && L > 0 && w >= p0 / R && w <= (p0 + L - 1) / R);
+        if (m) {
+            const int j = __builtin_ctzll(m);
+            s = b + j;
+            pj = __builtin_amdgcn_readlane(p0, j);
+            lj = __builtin_amdgcn_readlane(L, j);
+            break;
+        }
+        base += __builtin_amdgcn_readlane(inc, 63);
+    }
+    if (s < 0) return;   // no piece in this slot
+    const int w = k - s;
+    const int r0 = max(w * R - pj, 0), r1 = min((w + 1) * R - pj, lj);
+    attn_piece_mfw<DH, M>(a, kvh, s, r0, r1 - r0, r0 == 0 && r1 == lj, ((size_t)kvh * (a.bal + a.n) + k) * G);
+}
+
 // Merge of the splits of one (query head, vector) by NT threads:
 // mx = max_s m_s, L = sum_s l_s e^(m_s - mx), out = sum_s o_s e^(m_s - mx) / L.
 // Thread (d, sg) sums the splits s = sg (mod SG) for dim d; the SG partial
@@ -484,12 +779,30 @@ __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n
     const int tid = threadIdx.x;
     const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
     const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
-    const int nact = (L + a.split - 1) / a.split;
+    int nact;
+    size_t hb;   // partial of split (piece) s: hb + s * G
+    if (a.bal) {
+        // pieces w0 .. w1 of the balanced walk, at slots w0 + n .. w1 + n
+        const int lane = tid & 63;
+        const int l0 = attn_len(a, lane);
+        const int R = attn_bal_range(a, l0);
+        int pre = 0;   // line offset of vector n
+        for (int b = 0; b < n; b += 64) {
+            const int i = b + lane;
+            pre += i < n ? (b == 0 ? l0 : attn_len(a, i)) + ATT_BAL_PAD : 0;
+        }
+        const int p0 = wave_sum_i(pre) + ATT_BAL_PAD;
+        const int w0 = p0 / R;
+        nact = L > 0 ? (p0 + L - 1) / R - w0 + 1 : 0;
+        hb = ((size_t)kvh * (a.bal + a.n) + w0 + n) * G + h;
+    } else {
+        nact = (L + a.split - 1) / a.split;
+        hb = (((size_t)n * a.n_kv + kvh) * a.max_splits) * G + h;
+    }
     if (nact <= 1) return;
     __shared__ float wsh[ATT_MAX_MERGE];
     __shared__ float rsh[NT / 64];
     __shared__ float part[SG][DH];
-    const size_t hb = (((size_t)n * a.n_kv + kvh) * a.max_splits) * G + h;   // + s * G
     const int w = tid >> 6, lane = tid & 63;
     const int d = tid % DH, sg = tid / DH;
     const float m0 = tid < nact ? a.pm[hb + (size_t)tid * G] : -INFINITY;

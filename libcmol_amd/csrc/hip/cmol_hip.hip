@@ -492,6 +492,7 @@ int cmolhip_attn_decode(cmolhip_ctx_t *c, int n, const float *q, const void *kca
         a.kv_f16 = kv_f16;
         a.split = split;
         a.max_splits = ms;
+        a.bal = attn_bal_wgs(n, n_kv, d_head, kv_f16, ms);
         a.pm = pm;
         a.pl = pl;
         a.po = po;
@@ -1190,6 +1191,7 @@ int enqueue_step(cmolhip_model *m, Batch &B, int n, hipStream_t st)
         at.kv_f16 = hp.kv_f16;
         at.split = m->split;
         at.max_splits = m->max_splits;
+        at.bal = attn_bal_wgs(n, hp.n_kv_heads, hp.d_head, hp.kv_f16, m->max_splits);
         at.pm = B.pm;
         at.pl = B.pl;
         at.po = B.po;

@@ -274,6 +274,9 @@ struct AttnArgs {
     int n, n_heads, n_kv, d_head, max_ctx, kv_f16;
     int split;              // positions per work-group
     int max_splits;
+    int bal;                // > 0 (fp16 cache, d_head 64..256): bal balanced ranges per
+                            // kv head instead of one work-group per split; partials
+                            // [n_kv][bal + n][G]( [d_head]), bal + n <= n * max_splits
     float *pm, *pl, *po;    // partials [n][n_kv][max_splits][G]( [d_head])
     float *out;             // [n][out_stride] fp32, or nullptr
     int out_stride;
@@ -281,6 +284,13 @@ struct AttnArgs {
 };
 
 int launch_attn(const AttnArgs &a, hipStream_t s);
+// Balanced ranges per kv head (AttnArgs::bal) for n vectors over a cache
+// planned with max_splits splits, or 0 where they do not apply (one vector,
+// fp32 cache, d_head outside 64..256).  The grid is bal + n work-groups per
+// kv head; CMOL_ATTN_BAL=<total work-groups> sets it (0: off).  The
+// default is one round of the four work-groups a CU holds.
+#define ATT_BAL_WGS_PER_CU 4
+int attn_bal_wgs(int n, int n_kv, int d_head, int kv_f16, int max_splits);
 // Prompt-pass attention (flash style on MFMA) for vectors that are
 // consecutive tokens of one session over an fp32 cache, d_head 64 / 128;
 // returns -4 for shapes it does not take (the caller runs launch_attn).

@@ -294,6 +294,86 @@ def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens, split, 
         assert_close(got[i], want, f"attention session {i} len {L} split {split}")
 
 
+def attention_case(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16, seed):
+    n = len(lens)
+    max_ctx = max(lens)
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((n, n_heads * d_head)).astype(np.float32)
+    kc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
+    vc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
+    if kv_f16:
+        kc16, vc16 = kc.astype(np.float16), vc.astype(np.float16)
+        kc, vc = kc16.astype(np.float32), vc16.astype(np.float32)
+        dk, dv = ctx.upload(kc16), ctx.upload(vc16)
+    else:
+        dk, dv = ctx.upload(kc), ctx.upload(vc)
+    dq, ds = ctx.upload(q), ctx.upload(np.array(lens, np.int32))
+    dout = ctx.alloc(q.nbytes)
+    import ctypes as C
+    gpu.check(gpu.lib().cmolhip_attn_decode(ctx.h, n, C.c_void_p(dq), C.c_void_p(dk), C.c_void_p(dv),
+                                            C.c_void_p(ds), n_heads, n_kv, d_head, max_ctx, kv_f16,
+                                            split, C.c_void_p(dout)), "attn")
+    got = ctx.d2h(dout, q.shape, np.float32)
+    for i, L in enumerate(lens):
+        kref = np.ascontiguousarray(kc[i].transpose(1, 0, 2)[:L])
+        vref = np.ascontiguousarray(vc[i].transpose(1, 0, 2)[:L])
+        want = O.attention(q[i], kref, vref, L, n_heads, n_kv, d_head)
+        assert_close(got[i], want, f"attention session {i} len {L} split {split}")
+
+
+# Balanced ranges over an fp16 cache: CMOL_ATTN_BAL = total work-groups, so
+# bal = total / n_kv - n ranges per kv head (at most n * (splits - 1)); small
+# grids cut contexts into several pieces (and ranges across several
+# contexts), large ones clamp the range to the split; None: the default grid.
+_R = np.random.default_rng(99)
+BAL_CASES = [
+    (16, 4, 128, [4096, 1, 257, 1500], 256, None), (16, 4, 128, [4096, 1, 257, 1500], 256, "44"),
+    (16, 4, 128, [4096, 1, 257, 1500], 256, "100000"), (8, 4, 64, [77, 700, 3, 64, 65, 129], 64, "36"),
+    (8, 8, 256, [200, 77, 513], 128, "40"), (16, 2, 128, [1000, 3, 2000], 64, "14"),
+    (4, 4, 128, [513, 64], 256, "20"), (12, 4, 128, [1, 1, 1, 300, 2], 64, "32"),
+    (4, 2, 64, [int(x) for x in _R.integers(1, 300, 70)], 64, "200"),
+    (4, 2, 64, [int(x) for x in _R.integers(1, 300, 70)], 64, None),
+    (16, 4, 128, [int(x) for x in _R.integers(400, 3000, 9)], 128, "48"),
+]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d_head,lens,split,bal", BAL_CASES)
+def test_attention_balanced_matches_oracle(ctx, gpu, monkeypatch, n_heads, n_kv, d_head, lens, split, bal):
+    """Decode attention over the balanced ranges (one work-group per piece of
+    a context cut by the ranges, pieces merged per vector): every vector
+    against the oracle, over mixes of long, short, length-1 and 70
+    contexts."""
+    if bal is None:
+        monkeypatch.delenv("CMOL_ATTN_BAL", raising=False)
+    else:
+        monkeypatch.setenv("CMOL_ATTN_BAL", bal)
+    attention_case(ctx, gpu, n_heads, n_kv, d_head, lens, split, 1, seed=len(lens) * 31 + d_head + split)
+
+
+def test_attention_balanced_equals_split_grid_closely(ctx, gpu, monkeypatch):
+    """The balanced ranges and the one-work-group-per-split grid give the
+    same outputs up to fp32 summation order (same inputs, both paths)."""
+    import ctypes as C
+    n_heads, n_kv, d_head, split = 16, 4, 128, 256
+    lens = [5000, 17, 900, 2600, 1]
+    n, max_ctx = len(lens), max(lens)
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((n, n_heads * d_head)).astype(np.float32)
+    kc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float16)
+    vc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float16)
+    dk, dv, dq = ctx.upload(kc), ctx.upload(vc), ctx.upload(q)
+    ds = ctx.upload(np.array(lens, np.int32))
+    outs = []
+    for bal in ("0", "60"):
+        monkeypatch.setenv("CMOL_ATTN_BAL", bal)
+        dout = ctx.alloc(q.nbytes)
+        gpu.check(gpu.lib().cmolhip_attn_decode(ctx.h, n, C.c_void_p(dq), C.c_void_p(dk), C.c_void_p(dv),
+                                                C.c_void_p(ds), n_heads, n_kv, d_head, max_ctx, 1, split,
+                                                C.c_void_p(dout)), "attn")
+        outs.append(ctx.d2h(dout, q.shape, np.float32))
+    assert np.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-6)
+
+
 # ---- K-quants (Q4_K = 12, Q6_K = 14): super-blocks of 256 ------------------
 KQ_DEQ = [((16, 256), 1), ((37, 512), 1), ((64, 2048), 4), ((21, 1024), 8), ((5, 768), 2),
           ((130, 2048), 1)]
