@@ -16,16 +16,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a)
         attn_split<DH, KT, ATT_THREADS, StPlain>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
-// Balanced ranges of an fp16 cache (attn_bal_mf), four waves per piece
-// each on its own positions; held to four work-groups per CU at d_head
-// <= 128 (the grid is sized for that many).
-template <int DH>
-__global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(DH <= 128 ? 4 : 1)))
-void k_attn_bal(AttnArgs a)
-{
-    attn_bal_mf<DH, StPlain>(a, blockIdx.x, blockIdx.y);
-}
-
 template <int DH>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_merge(AttnArgs a)
 {
@@ -673,18 +663,6 @@ int launch_attn_prompt(const AttnArgs &a, _Float16 *kv_hl, int last, hipStream_t
 
 int attn_max_splits(int max_ctx, int split) { return (max_ctx + split - 1) / split; }
 
-int attn_bal_wgs(int n, int n_kv, int d_head, int kv_f16, int max_splits)
-{
-    if (n < 2 || !kv_f16 || (d_head != 64 && d_head != 128 && d_head != 256) || max_splits < 2 ||
-        max_splits + 1 > ATT_MAX_MERGE)
-        return 0;
-    const char *e = getenv("CMOL_ATTN_BAL");
-    const long t = e ? atol(e) : (long)ATT_BAL_WGS_PER_CU * attn_cus();
-    if (t <= 0) return 0;
-    const long w = std::max(1L, t / n_kv - n), cap = (long)n * (max_splits - 1);
-    return (int)std::min(w, cap);
-}
-
 int launch_attn(const AttnArgs &a, hipStream_t s)
 {
     const int G = a.n_heads / a.n_kv;
@@ -696,24 +674,7 @@ int launch_attn(const AttnArgs &a, hipStream_t s)
         return -4;
     if (a.max_splits > ATT_MAX_MERGE) return -4;
     dim3 grid(a.n_kv, a.max_splits, a.n), block(ATT_THREADS), mgrid(a.n_heads, a.n);
-    if (a.bal > 0) {
-        // a piece count is at most one above the split count
-        if (!a.kv_f16 || a.max_splits + 1 > ATT_MAX_MERGE || (long)a.bal + a.n > (long)a.n * a.max_splits)
-            return -4;
-        const dim3 bgrid(a.n_kv, a.bal + a.n);
-        switch (a.d_head) {
-        case 64: hipLaunchKernelGGL((k_attn_bal<64>), bgrid, block, 0, s, a); break;
-        case 128: hipLaunchKernelGGL((k_attn_bal<128>), bgrid, block, 0, s, a); break;
-        case 256: hipLaunchKernelGGL((k_attn_bal<256>), bgrid, block, 0, s, a); break;
-        default: return -4;
-        }
-        switch (a.d_head) {
-        case 64: hipLaunchKernelGGL((k_attn_merge<64>), mgrid, block, 0, s, a); break;
-        case 128: hipLaunchKernelGGL((k_attn_merge<128>), mgrid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((k_attn_merge<256>), mgrid, block, 0, s, a); break;
-        }
-        return hipGetLastError() == hipSuccess ? 0 : -4;
-    }
+    if (a.bal > 0) return launch_attn_bal(a, s);
 #define ATT(DHV)                                                                          \
     if (a.kv_f16) hipLaunchKernelGGL((k_attn<DHV, _Float16>), grid, block, 0, s, a);      \
     else hipLaunchKernelGGL((k_attn<DHV, float>), grid, block, 0, s, a);

@@ -771,35 +771,14 @@ __device__ __forceinline__ void attn_bal_mf(const AttnArgs &a, int kvh, int k)
 // (m, l) and of the thread's first MP o values is issued at once (one round
 // trip); longer merges read the rest in loops.  Sessions whose length fits
 // one split were finished by attn_split.
+// The merge proper, for nact > 1 partials at hb + s * G.
 template <int DH, int NT, typename M>
-__device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n)
+__device__ __forceinline__ void attn_merge_run(const AttnArgs &a, int hq, int n, int nact, size_t hb)
 {
     constexpr int SG = NT / DH;
     constexpr int MP = 24;   // o values per thread loaded with the (m, l) (48 splits at d_head 128)
     const int tid = threadIdx.x;
-    const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
-    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
-    int nact;
-    size_t hb;   // partial of split (piece) s: hb + s * G
-    if (a.bal) {
-        // pieces w0 .. w1 of the balanced walk, at slots w0 + n .. w1 + n
-        const int lane = tid & 63;
-        const int l0 = attn_len(a, lane);
-        const int R = attn_bal_range(a, l0);
-        int pre = 0;   // line offset of vector n
-        for (int b = 0; b < n; b += 64) {
-            const int i = b + lane;
-            pre += i < n ? (b == 0 ? l0 : attn_len(a, i)) + ATT_BAL_PAD : 0;
-        }
-        const int p0 = wave_sum_i(pre) + ATT_BAL_PAD;
-        const int w0 = p0 / R;
-        nact = L > 0 ? (p0 + L - 1) / R - w0 + 1 : 0;
-        hb = ((size_t)kvh * (a.bal + a.n) + w0 + n) * G + h;
-    } else {
-        nact = (L + a.split - 1) / a.split;
-        hb = (((size_t)n * a.n_kv + kvh) * a.max_splits) * G + h;
-    }
-    if (nact <= 1) return;
+    const int G = a.n_heads / a.n_kv;
     __shared__ float wsh[ATT_MAX_MERGE];
     __shared__ float rsh[NT / 64];
     __shared__ float part[SG][DH];
@@ -854,5 +833,37 @@ __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n
         if (a.next.q) act_put<M>(a.next, n, k, o);
     }
     __syncthreads();   // the LDS areas may be reused by the caller
+}
+
+template <int DH, int NT, typename M>
+__device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n)
+{
+    const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int nact = (L + a.split - 1) / a.split;
+    if (nact <= 1) return;
+    attn_merge_run<DH, NT, M>(a, hq, n, nact, (((size_t)n * a.n_kv + kvh) * a.max_splits) * G + h);
+}
+
+// The pieces w0 .. w1 of vector n in the balanced split, at slots
+// w0 + n .. w1 + n of its kv head.
+template <int DH, int NT, typename M>
+__device__ __forceinline__ void attn_merge_bal(const AttnArgs &a, int hq, int n)
+{
+    const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
+    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int lane = threadIdx.x & 63;
+    const int l0 = attn_len(a, lane);
+    const int R = attn_bal_range(a, l0);
+    int pre = 0;   // line offset of vector n
+    for (int b = 0; b < n; b += 64) {
+        const int i = b + lane;
+        pre += i < n ? (b == 0 ? l0 : attn_len(a, i)) + ATT_BAL_PAD : 0;
+    }
+    const int p0 = wave_sum_i(pre) + ATT_BAL_PAD;
+    const int w0 = p0 / R;
+    const int nact = L > 0 ? (p0 + L - 1) / R - w0 + 1 : 0;
+    if (nact <= 1) return;
+    attn_merge_run<DH, NT, M>(a, hq, n, nact, ((size_t)kvh * (a.bal + a.n) + w0 + n) * G + h);
 }
 
