@@ -130,9 +130,12 @@ int cmolhip_gemm_noalloc(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const flo
 size_t cmolhip_noalloc_scratch_bytes(void);
 
 /* Reference kernel seam replacement (cmol_matmul_fn_t semantics on host
- * memory): out[m][n] = A[m][k] . B[k][n], A raw GGUF rows.  Uses the
- * context arena for the transient copies; fails with CMOL_ERR_OOM when the
- * arena cannot hold them. */
+ * memory, src/cmol_internal.h:175-187): out[m][n] = A[m][k] . B[k][n], A raw
+ * GGUF rows.  Block formats need k a multiple of 32; F32 (dtype 0) and F16
+ * (dtype 1) rows take any k and give the reference AVX-512 kernel's results
+ * bit for bit (src/quant.c:506-530).  Uses the context arena for the
+ * transient copies; fails with CMOL_ERR_OOM when the arena cannot hold
+ * them. */
 int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a,
                         const float *b, int m, int k, int n, int dtype);
 

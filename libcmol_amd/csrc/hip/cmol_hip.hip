@@ -421,9 +421,38 @@ int cmolhip_gemm_noalloc(cmolhip_ctx_t *c, const cmolhip_qtensor_t *w, const flo
     return launch_product(c, w, base, n, ss, eps, dy, part, pf, nullptr, nullptr);
 }
 
+// F32 / F16 weights: rows of k values, any k (src/quant.c:246-256)
+static int matmul_dense_host(cmolhip_ctx_t *c, float *out, const void *a, const float *b, int m, int k, int n,
+                             int dtype)
+{
+    const size_t esz = dtype == 0 ? 4 : 2;
+    const size_t mark = arena_mark(c);
+    int rc = E_OK;
+    do {
+        void *da = nullptr;
+        float *db = nullptr, *dx = nullptr, *dy = nullptr;
+        if ((rc = cmolhip_alloc(c, esz * (size_t)m * k, ALIGN, &da))) break;
+        if ((rc = arena_get(c, (size_t)k * n, &db))) break;
+        if ((rc = arena_get(c, (size_t)k * n, &dx))) break;
+        if ((rc = arena_get(c, (size_t)m * n, &dy))) break;
+        if ((rc = cmolhip_memcpy_h2d(c, da, a, esz * (size_t)m * k))) break;
+        if ((rc = cmolhip_memcpy_h2d(c, db, b, (size_t)k * n * 4))) break;
+        if ((rc = launch_transpose(db, dx, k, n, c->stream))) break;
+        if (launch_matmul_dense(da, dtype, dx, dy, m, k, n, c->stream)) {
+            rc = E_ARGS;
+            break;
+        }
+        if ((rc = cmolhip_memcpy_d2h(c, out, dy, (size_t)m * n * 4))) break;
+    } while (0);
+    arena_release(c, mark);
+    return rc;
+}
+
 int cmolhip_matmul_host(cmolhip_ctx_t *c, float *out, const void *a, const float *b, int m, int k,
                         int n, int dtype)
 {
+    if ((dtype == 0 || dtype == 1) && c && out && a && b && m >= 1 && k >= 1 && n >= 1 && n <= GEMM_MAX_N)
+        return matmul_dense_host(c, out, a, b, m, k, n, dtype);
     if (!c || !out || !a || !b || m < 1 || k < 32 || k % 32 || n < 1 || n > GEMM_MAX_N) return E_ARGS;
     if (!qbytes_aligned(dtype, m, k, 1)) return E_UNSUPPORTED;
     const size_t mark = arena_mark(c);

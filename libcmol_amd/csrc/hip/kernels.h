@@ -437,6 +437,9 @@ int persist_capacity_q8(int d_head, int kv_f16, int lds);
 // ---- misc.hip
 // dst[cols][rows] = transpose of src[rows][cols] (fp32).
 int launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s);
+// The kernel seam's F32 (dtype 0) and F16 (dtype 1) weight products:
+// out[m][n] = A[m][k] . x[n][k]^T in the reference AVX-512 kernel's order.
+int launch_matmul_dense(const void *a, int dtype, const float *x, float *out, int m, int k, int n, hipStream_t s);
 // out[i] = i, i < n.
 int launch_iota(int32_t *out, int n, hipStream_t s);
 int launch_kv_synth(void *kc, void *vc, int n_kv, int max_ctx, int d_head,

@@ -528,4 +528,47 @@ def test_matmul_host_seam_rejects_bad_arguments(gpu, ctx):
     assert L.cmolhip_matmul_host(ctx.h, *args, 4, 31, 1, 2) == gpu.CMOL_ERR_ARGS
     assert L.cmolhip_matmul_host(ctx.h, *args, 4, 32, 0, 2) == gpu.CMOL_ERR_ARGS
     assert L.cmolhip_matmul_host(ctx.h, None, raw.ctypes.data, b.ctypes.data, 4, 32, 1, 2) == gpu.CMOL_ERR_ARGS
-    assert L.cmolhip_matmul_host(ctx.h, *args, 4, 32, 1, 0) == gpu.CMOL_ERR_UNSUPPORTED
+    assert L.cmolhip_matmul_host(ctx.h, *args, 4, 32, 1, 3) == gpu.CMOL_ERR_UNSUPPORTED
+    assert L.cmolhip_matmul_host(ctx.h, *args, 4, 0, 1, 0) == gpu.CMOL_ERR_ARGS   # F32, k = 0
+
+
+def test_matmul_host_seam_f32_reference_kats(gpu, ctx):
+    """The reference's own F32 matmul checks (tests/test_quant.c:210-261):
+    m=3, k=4, n=1 and m=2, k=4, n=2, exact."""
+    L = gpu.lib()
+    a = np.array([[1, 0, 0, 0], [0, 1, 0, 0], [1, 1, 0, 0]], np.float32)
+    b = np.array([5, 7, 0, 0], np.float32).reshape(4, 1)
+    out = np.zeros((3, 1), np.float32)
+    gpu.check(L.cmolhip_matmul_host(ctx.h, gpu.ptr(out), gpu.ptr(a), gpu.ptr(b), 3, 4, 1, 0), "f32 kat")
+    assert out.ravel().tolist() == [5.0, 7.0, 12.0]
+    a2 = np.ascontiguousarray(a[:2])
+    b2 = np.array([1, 2, 3, 4, 0, 0, 0, 0], np.float32).reshape(4, 2)
+    out2 = np.zeros((2, 2), np.float32)
+    gpu.check(L.cmolhip_matmul_host(ctx.h, gpu.ptr(out2), gpu.ptr(a2), gpu.ptr(b2), 2, 4, 2, 0), "f32 kat n2")
+    assert out2.ravel().tolist() == [1.0, 2.0, 3.0, 4.0]
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("m,k,n", [(7, 4, 1), (33, 100, 3), (64, 2048, 1), (130, 515, 5), (16, 16, 40),
+                                   (5, 31, 2), (300, 4096, 1)])
+def test_matmul_host_seam_dense_bit_exact(gpu, ctx, dtype, m, k, n):
+    """F32 and F16 weights through the seam (src/quant.c:351-360, 506-530):
+    bit-identical to the oracle's AVX-512-order restatement (sixteen fused
+    accumulators, the _mm512_reduce_add_ps tree, an unfused tail; F16 one
+    unfused running sum), for any k, F16 rows including subnormal halves."""
+    L = gpu.lib()
+    rng = np.random.default_rng(m * 1000 + k * 7 + n + dtype)
+    if dtype == 0:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+    else:
+        a = rng.standard_normal((m, k)).astype(np.float16)
+        sub = rng.random((m, k)) < 0.05   # subnormal halves
+        a[sub] = (rng.integers(1, 1024, int(sub.sum())).astype(np.uint16)).view(np.float16)
+        a = a.view(np.uint16)
+    a = np.ascontiguousarray(a)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    out = np.zeros((m, n), np.float32)
+    gpu.check(L.cmolhip_matmul_host(ctx.h, gpu.ptr(out), gpu.ptr(a), gpu.ptr(b), m, k, n, dtype), "dense seam")
+    want = O.matmul(a.view(np.uint8), b, m, k, dtype, O.AVX512)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32)), \
+        f"dtype {dtype} {m}x{k} n {n}: max diff {np.abs(out - want).max():.3g}"
