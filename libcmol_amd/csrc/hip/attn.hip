@@ -635,7 +635,14 @@ int launch_attn_prompt_dh(const AttnArgs &a, _Float16 *kv_hl, int last, hipStrea
                        kv_hl, tiles);
     const dim3 grid(a.n_kv, (a.n + QT - 1) / QT, a.max_splits), block(256), mgrid(a.n_heads, a.n);
     hipLaunchKernelGGL(k_attn_prompt<DH>, grid, block, attn_prompt_lds<DH>(), s, a, kv_hl, tiles);
-    if (a.max_splits > 1) hipLaunchKernelGGL((k_attn_merge<DH>), mgrid, block, 0, s, a);
+    if (a.max_splits > 1) {
+        static const bool wave = [] {   // CMOL_PROMPT_MERGE=1: the work-group merge (measurements)
+            const char *e = getenv("CMOL_PROMPT_MERGE");
+            return !(e && e[0] == '1');
+        }();
+        if (wave) return launch_attn_merge_wave(a, s);
+        hipLaunchKernelGGL((k_attn_merge<DH>), mgrid, block, 0, s, a);
+    }
     return 0;
 }
 

@@ -90,27 +90,32 @@ size_t gemv_part_floats(const QTensor &w, int n)
     return f;
 }
 
-// k-split finish: one wave per (64 rows, vector); lane l takes row 64*bx + l,
-// so the lanes of a 16-row tile are a 16-lane group, as the epilogues need.
-// The epilogue's own inputs and the first FS slices' partial sums are
-// loaded together, unconditionally (rows past the matrix re-read the last
-// one), so the kernel waits for one round trip before the epilogue.
-#define FS 16
-template <int EPI>
+// k-split finish: each wave takes RPT runs of 64 rows of one vector; lane
+// l takes row l of each run, so the lanes of a 16-row tile are a 16-lane
+// group, as the epilogues need.  The epilogue's own inputs and the first
+// FS slices' partial sums of every run are loaded together,
+// unconditionally (rows past the matrix re-read the last one), so the
+// kernel waits for one round trip before the epilogues.  Four runs per
+// wave (FS = 4: the prompt GEMM's k ranges) serve the large finishes of
+// prompt passes with a quarter of the work-groups.
+template <int EPI, int RPT, int FS>
 __global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, int ss_count)
 {
 #pragma clang fp contract(off)
     const int v = blockIdx.y, l = threadIdx.x & 63;
-    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + l;
-    if ((row & ~63) >= a.w.rows) return;   // whole waves past the matrix
-    const bool act = row < a.w.rows;
-    EpiPre pre;
-    epi_pre_load(a, EPI, v, row, act, pre);
-    const float *pp = a.part + (size_t)v * a.w.rows + min(row, a.w.rows - 1);
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 * RPT;   // the wave's first row
+    if (r0 >= a.w.rows) return;   // whole waves past the matrix
     const size_t kstride = (size_t)a.n * a.w.rows;
-    float pv[FS];
+    EpiPre pre[RPT];
+    float pv[RPT][FS];
 #pragma unroll
-    for (int k = 0; k < FS; k++) pv[k] = pp[(size_t)min(k, splits - 1) * kstride];
+    for (int p = 0; p < RPT; p++) {
+        const int row = r0 + 64 * p + l;
+        epi_pre_load(a, EPI, v, row, row < a.w.rows, pre[p]);
+        const float *pp = a.part + (size_t)v * a.w.rows + min(row, a.w.rows - 1);
+#pragma unroll
+        for (int k = 0; k < FS; k++) pv[p][k] = pp[(size_t)min(k, splits - 1) * kstride];
+    }
     float nrm = 1.0f;
     if (ss_count) {
         float s = 0.0f;
@@ -118,32 +123,52 @@ __global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, i
         s = wave_sum(s);
         nrm = 1.0f / sqrtf(s / (float)a.w.cols + a.in.eps);
     }
-    epi_pre_cs(a, EPI, row, act, pre);
-    // slices added in ascending order
-    float y = 0.0f;
 #pragma unroll
-    for (int k = 0; k < FS; k++)
-        if (k < splits) y += pv[k];
-    for (int k = FS; k < splits; k++) y += pp[(size_t)k * kstride];
-    y *= nrm;
-    epilogue<EPI>(a, row >> 4, row & 15, 16, v, act, y, true, pre);
+    for (int p = 0; p < RPT; p++) {
+        const int row = r0 + 64 * p + l;
+        if (r0 + 64 * p >= a.w.rows) break;   // uniform
+        const bool act = row < a.w.rows;
+        epi_pre_cs(a, EPI, row, act, pre[p]);
+        // slices added in ascending order
+        float y = 0.0f;
+#pragma unroll
+        for (int k = 0; k < FS; k++)
+            if (k < splits) y += pv[p][k];
+        const float *pp = a.part + (size_t)v * a.w.rows + min(row, a.w.rows - 1);
+        for (int k = FS; k < splits; k++) y += pp[(size_t)k * kstride];
+        y *= nrm;
+        epilogue<EPI>(a, row >> 4, row & 15, 16, v, act, y, true, pre[p]);
+    }
 }
-#undef FS
 
-int launch_gemv_b_finish(const GemvArgs &a, int epi, int splits, int ss_count, hipStream_t s)
+template <int RPT, int FS>
+static void launch_finish(const GemvArgs &a, int epi, int splits, int ss_count, hipStream_t s)
 {
-    const dim3 grid((a.w.rows + 255) / 256, a.n), block(256);
+    const dim3 grid((a.w.rows + 256 * RPT - 1) / (256 * RPT), a.n), block(256);
     auto go = [&](auto kern) {
         if (a.ev_stop) hipExtLaunchKernelGGL(kern, grid, block, 0, s, nullptr, a.ev_stop, 0, a, splits, ss_count);
         else hipLaunchKernelGGL(kern, grid, block, 0, s, a, splits, ss_count);
     };
     switch (epi) {
-    case EPI_STORE: go(k_gemv_b_finish<EPI_STORE>); break;
-    case EPI_RESID: go(k_gemv_b_finish<EPI_RESID>); break;
-    case EPI_SWIGLU: go(k_gemv_b_finish<EPI_SWIGLU>); break;
-    case EPI_QKV: go(k_gemv_b_finish<EPI_QKV>); break;
-    default: go(k_gemv_b_finish<EPI_LOGITS>); break;
+    case EPI_STORE: go(k_gemv_b_finish<EPI_STORE, RPT, FS>); break;
+    case EPI_RESID: go(k_gemv_b_finish<EPI_RESID, RPT, FS>); break;
+    case EPI_SWIGLU: go(k_gemv_b_finish<EPI_SWIGLU, RPT, FS>); break;
+    case EPI_QKV: go(k_gemv_b_finish<EPI_QKV, RPT, FS>); break;
+    default: go(k_gemv_b_finish<EPI_LOGITS, RPT, FS>); break;
     }
+}
+
+int launch_gemv_b_finish(const GemvArgs &a, int epi, int splits, int ss_count, hipStream_t s)
+{
+    // four runs per wave where the one-run grid would take several rounds
+    // of the CUs (prompt passes: 512 vectors x 2048 rows, 4096 work-groups)
+    static const bool wide = [] {
+        const char *e = getenv("CMOL_FINISH_RUNS");   // measurements: 1 turns it off
+        return !(e && e[0] == '1');
+    }();
+    const long wgs = (long)((a.w.rows + 255) / 256) * a.n;
+    if (wide && splits <= 4 && wgs >= 8L * gemv_cus()) launch_finish<4, 4>(a, epi, splits, ss_count, s);
+    else launch_finish<1, 16>(a, epi, splits, ss_count, s);
     return 0;
 }
 

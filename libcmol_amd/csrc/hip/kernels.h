@@ -292,6 +292,9 @@ int launch_attn(const AttnArgs &a, hipStream_t s);
 #define ATT_BAL_WGS_PER_CU 4
 int attn_bal_wgs(int n, int n_kv, int d_head, int kv_f16, int max_splits);
 int launch_attn_bal(const AttnArgs &a, hipStream_t s);   // a.bal > 0 (launch_attn calls it)
+// The split merge with one wave per (query head, vector), d_head 64 / 128:
+// prompt passes (the split layout of launch_attn).
+int launch_attn_merge_wave(const AttnArgs &a, hipStream_t s);
 // Prompt-pass attention (flash style on MFMA) for vectors that are
 // consecutive tokens of one session over an fp32 cache, d_head 64 / 128;
 // returns -4 for shapes it does not take (the caller runs launch_attn).
