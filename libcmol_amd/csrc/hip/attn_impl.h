@@ -476,7 +476,11 @@ __device__ __forceinline__ void attn_piece_mf(const AttnArgs &a, int kvh, int n,
 //   * lazy online softmax: a head's reference maximum m moves only when a
 //     score exceeds it by more than ATT_LAZY_T (a wave vote), so the common
 //     step needs no cross-lane reduction; weights e = exp(s - m) <= e^T stay
-//     exact f16 pairs (hi + lo/2048) and each lane sums its own e;
+//     exact f16 pairs (hi + lo/2048) and each lane sums its own e; scores
+//     and m stay raw dot products t (m leaves the piece scaled), and e is
+//     2^(t c - m c), c = log2(e)/sqrt(d_head), on the hardware exponential
+//     (one FMA and v_exp_f32, whose exp2(-inf) = 0 also clears masked
+//     positions), the product m c taken once per move of m;
 //   * weighted sum P . V on 16x16x16 MFMAs: the wave's 16 V rows are staged
 //     in its own LDS rows (padded by four halves) and each B column (one
 //     dimension, four positions) is one transposing LDS read.
@@ -494,9 +498,11 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
     constexpr int DT = DH / 16;           // 16-dimension output tiles
     constexpr int RS = DH + 4;            // LDS row stride of the staged V (halves)
     static_assert(DH >= 64 && DH % 64 == 0 && VPL >= 1, "shape");
-    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wid = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int col = lane & 15, grp = lane >> 4, part = col & 1;
     const int G = a.n_heads / a.n_kv;
+    cnt = __builtin_amdgcn_readfirstlane(cnt);   // the same in every lane
+    t0 = __builtin_amdgcn_readfirstlane(t0);
     const int nst = (cnt + 63) / 64;
 
     __shared__ __attribute__((aligned(16))) _Float16 vsw[NW][16 * RS];
@@ -506,21 +512,24 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
     float *xo = (float *)vsw;
 
     const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
-    const _Float16 *kb = (const _Float16 *)a.kv.k_base + off;
-    const _Float16 *vb = (const _Float16 *)a.kv.v_base + off;
+    const _Float16 *kb = uniform_ptr((const _Float16 *)a.kv.k_base + off);
+    const _Float16 *vb = uniform_ptr((const _Float16 *)a.kv.v_base + off);
     f16x8 km[KS], vm[VPL];
+    // 32-bit byte offsets from the piece's (uniform) base: the loads take
+    // the base from scalar registers and need no 64-bit address arithmetic
+    const char *kbc = (const char *)kb, *vbc = (const char *)vb;
     auto load_k = [&](int j) {
-        const int p = min(64 * j + 16 * wid + col, cnt - 1);
+        const unsigned p = (unsigned)min(64 * j + 16 * wid + col, cnt - 1);
 #pragma unroll
-        for (int s = 0; s < KS; s++) km[s] = ldg((const f16x8 *)(kb + (size_t)p * DH + 32 * s + 8 * grp));
+        for (int s = 0; s < KS; s++) km[s] = ldg((const f16x8 *)(kbc + 2u * (p * DH + 32 * s + 8 * grp)));
     };
     // piece q = lane + 64i: row q / PPR of the step, dimensions 8 (q % PPR) .. +7
     auto load_v = [&](int j) {
 #pragma unroll
         for (int i = 0; i < VPL; i++) {
             const int q = lane + 64 * i;
-            const int p = min(64 * j + 16 * wid + q / PPR, cnt - 1);
-            vm[i] = ldg((const f16x8 *)(vb + (size_t)p * DH + 8 * (q % PPR)));
+            const unsigned p = (unsigned)min(64 * j + 16 * wid + q / PPR, cnt - 1);
+            vm[i] = ldg((const f16x8 *)(vbc + 2u * (p * DH + 8 * (q % PPR))));
         }
     };
     // B operand of the scores: lane l feeds column l%16 (head (l%16)/2, high
@@ -554,7 +563,12 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
     f32x4 oc[DT];
 #pragma unroll
     for (int t = 0; t < DT; t++) oc[t] = zero4;
+    // scores stay as raw dot products t (the scale folds into the
+    // exponent): e = 2^(t c - m c) with c = scale log2(e), m in raw units
+    constexpr float L2E = 1.44269504088896341f;   // log2(e)
+    const float c2 = scale * L2E, lazy = ATT_LAZY_T / scale;
     float m = -INFINITY, lsum = 0.0f;   // head rh of this lane's column
+    float mk = INFINITY;                // -m c
     _Float16 *vme = vsw[wid];
 
     for (int j = 0; j < nst; j++) {
@@ -574,8 +588,9 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
         }
         if (j + 1 < nst) load_v(j + 1);
         if (pb >= cnt) continue;   // every row of the wave past the piece (uniform)
-        // scores of positions pb + 4 grp + i: the high and low parts meet
-        // across the lane pair (l, l ^ 1)
+        // raw scores of positions pb + 4 grp + i: the high and low parts
+        // meet across the lane pair (l, l ^ 1); hi + lo / 2048 in one FMA
+        // (the product is exact)
         float sv[4];
         bool up = false;
 #pragma unroll
@@ -583,8 +598,8 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
             const float other = __int_as_float(
                 __builtin_amdgcn_mov_dpp(__float_as_int(sc[i]), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
             const float hi = part ? other : sc[i], lo = part ? sc[i] : other;
-            sv[i] = pb + 4 * grp + i < cnt ? (hi + lo * (1.0f / 2048.0f)) * scale : -INFINITY;
-            up |= sv[i] > m + ATT_LAZY_T;
+            sv[i] = pb + 4 * grp + i < cnt ? fmaf(lo, 1.0f / 2048.0f, hi) : -INFINITY;
+            up |= sv[i] > m + lazy;
         }
         if (__ballot(up)) {
             // new reference maxima: the column's maximum over the 16 positions
@@ -592,8 +607,10 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
             cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
             cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
             const float mn = fmaxf(m, cm);
-            const float al = mn == m ? 1.0f : expf(m - mn);
+            const float mkn = -mn * c2;
+            const float al = mn == m ? 1.0f : __builtin_amdgcn_exp2f(mkn - mk);
             m = mn;
+            mk = mkn;
             lsum *= al;
             // the output rows of this lane: heads 2 grp and 2 grp + 1, whose
             // factors sit in the lanes of columns 4 grp and 4 grp + 2
@@ -609,7 +626,7 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
         f16x4 pa;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float e = sv[i] > -INFINITY ? expf(sv[i] - m) : 0.0f;
+            const float e = __builtin_amdgcn_exp2f(fmaf(sv[i], c2, mk));
             lsum += e;
             const _Float16 ehi = (_Float16)e;
             pa[i] = part ? (_Float16)((e - (float)ehi) * 2048.0f) : ehi;
@@ -632,7 +649,7 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
     lsum += __shfl_xor(lsum, 32, 64);
     __syncthreads();   // every wave done with its V rows: the area takes the outputs
     if (grp == 0 && !part && rh < G) {
-        xm[wid][rh] = m;
+        xm[wid][rh] = m * scale;   // natural units, as the partials carry it
         xl[wid][rh] = lsum;
     }
 #pragma unroll

@@ -40,6 +40,17 @@ __device__ __forceinline__ __attribute__((address_space(1))) T *gptr(T *p)
 
 // Load of a 4-, 8- or 16-byte value (vector class types included) through
 // gptr.
+// A pointer every lane holds the same value of, moved to scalar registers
+// (loads through it can take the base from there: no per-lane 64-bit adds).
+template <typename T>
+__device__ __forceinline__ const T *uniform_ptr(const T *p)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const T *)(((uint64_t)hi << 32) | lo);
+}
+
 template <typename T>
 __device__ __forceinline__ T ldg(const T *p)
 {
