@@ -446,7 +446,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int last = min(a.seqlen[(size_t)(vb + nt - 1) * a.seqlen_stride], a.max_ctx);   // positions 0 .. last-1
     const int pa = sp * a.split, pb = min(pa + a.split, last);   // this split's positions
     if (pa >= last) return;
-    const float scale = 1.0f / sqrtf((float)DH);
+    // scores and m stay raw dot products; a weight is 2^(t c - m c) with
+    // c = log2(e)/sqrt(d_head) on the hardware exponential (exp2(-inf) = 0)
+    const float scale = 1.0f / sqrtf((float)DH), c2 = scale * 1.44269504088896341f;
     const uint8_t *tsrc = (const uint8_t *)(hl + ((size_t)kvh * tiles + pa / TP) * TH);
     // tile j of the split into stage st: 4 x PIECES pieces of 1 KiB
     auto issue = [&](int st, int j) {
@@ -517,7 +519,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int pos = p0 + 16 * c + 4 * g + i;
-                sc[c][i] = pos < lim ? (s1[i] + s2[i] * (1.0f / 2048.0f)) * scale : -INFINITY;
+                sc[c][i] = pos < lim ? fmaf(s2[i], 1.0f / 2048.0f, s1[i]) : -INFINITY;   // raw score
             }
         }
         // ---- online softmax of the row: its 32 scores are in lanes col,
@@ -532,14 +534,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const float mn = fmaxf(m, mx);
         // a row with no visible position yet keeps m = -inf: weights 0
         const float mref = mn == -INFINITY ? 0.0f : mn;
-        const float alpha = expf(m - mref);
+        const float alpha = __builtin_amdgcn_exp2f((m - mref) * c2);
+        const float mk = -mref * c2;
         float ps = 0.0f;
         f16x8 ph, pl;
 #pragma unroll
         for (int c = 0; c < 2; c++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float e = expf(sc[c][i] - mref);
+                const float e = __builtin_amdgcn_exp2f(fmaf(sc[c][i], c2, mk));
                 ps += e;
                 const _Float16 eh = (_Float16)e;
                 ph[4 * c + i] = eh;
@@ -596,7 +599,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             *(float4 *)&a.po[sb * DH + 16 * t + 4 * g] = ov;
         }
         if (g == 0) {
-            a.pm[sb] = m;
+            a.pm[sb] = m * scale;   // natural units, as the merge reads them
             a.pl[sb] = lsum;
         }
     }
