@@ -151,7 +151,7 @@ __device__ inline f16x8 pack8(f16x2 a, f16x2 b, f16x2 c, f16x2 d)
 __device__ inline uint32_t magic_1024()
 {
     uint32_t m = 0x64006400u;
-    asm volatile("" : "+v"(m));   // keep in a VGPR so and-or fuses
+    asm("" : "+v"(m));   // in a VGPR so and-or fuses; not volatile, so one copy serves every decode
     return m;
 }
 
