@@ -488,7 +488,7 @@ __device__ __forceinline__ void attn_piece_mf(const AttnArgs &a, int kvh, int n,
 #define ATT_LAZY_T 8.0f
 template <int DH, typename M>
 __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n, int t0, int cnt, bool single,
-                                               size_t sbase)
+                                               size_t sbase, size_t kvo)
 {
 #pragma clang fp contract(off)
     constexpr int NT = 256, NW = NT / 64;
@@ -511,7 +511,7 @@ __device__ __forceinline__ void attn_piece_mfw(const AttnArgs &a, int kvh, int n
     __shared__ float xm[NW][ATT_MAX_G], xl[NW][ATT_MAX_G];
     float *xo = (float *)vsw;
 
-    const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
+    const size_t off = kvo + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;   // kvo: the vector's cache base
     const _Float16 *kb = uniform_ptr((const _Float16 *)a.kv.k_base + off);
     const _Float16 *vb = uniform_ptr((const _Float16 *)a.kv.v_base + off);
     f16x8 km[KS], vm[VPL];
@@ -757,10 +757,13 @@ __device__ __forceinline__ void attn_bal_mf(const AttnArgs &a, int kvh, int k)
     const int l0 = attn_len(a, lane);
     const int R = attn_bal_range(a, l0);
     // the piece (w, s) with w + s = k: vector s's pieces are w0 .. w1
-    // (wave scans over blocks of 64 vectors; at most one lane matches)
-    int base = 0, s = -1, pj = 0, lj = 0;
+    // (wave scans over blocks of 64 vectors; at most one lane matches).
+    // Each lane also loads its vector's cache slot beside its length, so
+    // the piece's K/V addresses wait for no further load.
+    int base = 0, s = -1, pj = 0, lj = 0, sj = 0;
     for (int b = 0; b < a.n; b += 64) {
         const int L = b == 0 ? l0 : attn_len(a, b + lane);
+        const int slot = a.kv.slot_ids && b + lane < a.n ? a.kv.slot_ids[b + lane] : 0;
         const int v = b + lane < a.n ? L + ATT_BAL_PAD : 0;
         const int inc = wave_scan_i(v);
         const int p0 = base + inc - v + ATT_BAL_PAD;   // line offset of the vector's position 0
@@ -771,6 +774,7 @@ __device__ __forceinline__ void attn_bal_mf(const AttnArgs &a, int kvh, int k)
             s = b + j;
             pj = __builtin_amdgcn_readlane(p0, j);
             lj = __builtin_amdgcn_readlane(L, j);
+            sj = __builtin_amdgcn_readlane(slot, j);
             break;
         }
         base += __builtin_amdgcn_readlane(inc, 63);
@@ -778,7 +782,8 @@ __device__ __forceinline__ void attn_bal_mf(const AttnArgs &a, int kvh, int k)
     if (s < 0) return;   // no piece in this slot
     const int w = k - s;
     const int r0 = max(w * R - pj, 0), r1 = min((w + 1) * R - pj, lj);
-    attn_piece_mfw<DH, M>(a, kvh, s, r0, r1 - r0, r0 == 0 && r1 == lj, ((size_t)kvh * (a.bal + a.n) + k) * G);
+    const size_t kvo = (a.kv.slot_ids ? (size_t)sj * a.kv.slot_stride : 0) + a.kv.layer_off;
+    attn_piece_mfw<DH, M>(a, kvh, s, r0, r1 - r0, r0 == 0 && r1 == lj, ((size_t)kvh * (a.bal + a.n) + k) * G, kvo);
 }
 
 // Merge of the splits of one (query head, vector) by NT threads:
