@@ -63,14 +63,34 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
     const int kvh = blockIdx.x, sp = blockIdx.y, n = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the prologue's launch arguments in one batch of loads, then the
+    // vector's length and cache slot together (the slot read from a valid
+    // address either way): two round trips before the K/V loads, not four
+    sgpr_pin(a.seqlen);
+    sgpr_pin(a.seqlen_stride);
+    sgpr_pin(a.max_ctx);
+    sgpr_pin(a.split);
+    sgpr_pin(a.kv.k_base);
+    sgpr_pin(a.kv.v_base);
+    sgpr_pin(a.kv.slot_ids);
+    sgpr_pin(a.kv.slot_stride);
+    sgpr_pin(a.kv.layer_off);
+    sgpr_pin(a.q);
+    sgpr_pin(a.q_stride);
+    const int32_t *lenp = a.seqlen + (size_t)n * a.seqlen_stride;
+    const int32_t *slotp = a.kv.slot_ids ? a.kv.slot_ids + n : lenp;
+    const int len = *lenp, slot = *slotp;
+    sgpr_pin(len);
+    sgpr_pin(slot);
     const int G = a.n_heads / a.n_kv;
-    const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
+    const int L = min(len, a.max_ctx);
     const int t0 = sp * a.split;
     if (t0 >= L) return;
     const int cnt = min(L, t0 + a.split) - t0;
     const int nch = (cnt + CH - 1) / CH;
     const int nact = (L + a.split - 1) / a.split;
-    const size_t off = kv_offset(a.kv, n) + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
+    const size_t kvo = (a.kv.slot_ids ? (size_t)slot * a.kv.slot_stride : 0) + a.kv.layer_off;
+    const size_t off = kvo + (size_t)kvh * a.max_ctx * DH + (size_t)t0 * DH;
     const uint8_t *kb = (const uint8_t *)((const KT *)a.kv.k_base + off);
     const uint8_t *vb = (const uint8_t *)((const KT *)a.kv.v_base + off);
 

@@ -860,6 +860,18 @@ __device__ __forceinline__ void attn_merge_run(const AttnArgs &a, int hq, int n,
 template <int DH, int NT, typename M>
 __device__ __forceinline__ void attn_merge_head(const AttnArgs &a, int hq, int n)
 {
+    // the launch arguments the partial loads need, in the same batch as
+    // the length's (not in a second round trip after it)
+    sgpr_pin(a.seqlen);
+    sgpr_pin(a.seqlen_stride);
+    sgpr_pin(a.max_ctx);
+    sgpr_pin(a.split);
+    sgpr_pin(a.n_heads);
+    sgpr_pin(a.n_kv);
+    sgpr_pin(a.max_splits);
+    sgpr_pin(a.pm);
+    sgpr_pin(a.pl);
+    sgpr_pin(a.po);
     const int G = a.n_heads / a.n_kv, kvh = hq / G, h = hq % G;
     const int L = min(a.seqlen[n * a.seqlen_stride], a.max_ctx);
     const int nact = (L + a.split - 1) / a.split;

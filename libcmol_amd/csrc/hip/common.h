@@ -40,6 +40,16 @@ __device__ __forceinline__ __attribute__((address_space(1))) T *gptr(T *p)
 
 // Load of a 4-, 8- or 16-byte value (vector class types included) through
 // gptr.
+// Pins a launch argument in SGPRs at this point: the kernel-argument loads
+// of every pinned value are then issued together and waited for once,
+// instead of being sunk into the branches that first use them (each sunk
+// group is another round trip before the weight loads go out).
+template <typename T>
+__device__ __forceinline__ void sgpr_pin(T v)
+{
+    asm volatile("" ::"s"(v));
+}
+
 // A pointer every lane holds the same value of, moved to scalar registers
 // (loads through it can take the base from there: no per-lane 64-bit adds).
 template <typename T>

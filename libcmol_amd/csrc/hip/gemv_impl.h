@@ -209,16 +209,6 @@ __device__ __forceinline__ void epi_pre_cs(const GemvArgs &a, int epi, int row, 
     }
 }
 
-// Pins a launch argument in SGPRs at this point: the kernel-argument loads
-// of every pinned value are then issued together and waited for once,
-// instead of being sunk into the branches that first use them (each sunk
-// group is another round trip before the weight loads go out).
-template <typename T>
-__device__ __forceinline__ void sgpr_pin(T v)
-{
-    asm volatile("" ::"s"(v));
-}
-
 // Epilogue for vector v, weight row R*t + rl.  Every lane of the wave calls
 // it (shuffles within aligned groups of R lanes, one group per (vector,
 // tile)); `act` marks lanes whose (row, v) is real.  With `has_pre`, `pre`
