@@ -305,13 +305,17 @@ void k_gemv(GemvArgs a, GemvShape sh)
     sgpr_pin(a.in.ss_stride);
     sgpr_pin(sh.qpc);
     sgpr_pin(sh.zslot);
-    sgpr_pin(sh.epi);
     sgpr_pin(a.out);
-    sgpr_pin(a.res);
     sgpr_pin(a.out_stride);
-    sgpr_pin(a.pos);
-    sgpr_pin(a.pos_stride);
-    sgpr_pin(a.kv.slot_ids);
+    // the epilogue's own arguments only where it can use them (fewer loads
+    // in the batch)
+    if constexpr (EPI < 0) sgpr_pin(sh.epi);
+    if constexpr (EPI < 0 || EPI == EPI_RESID) sgpr_pin(a.res);
+    if constexpr (EPI < 0 || EPI == EPI_QKV) {
+        sgpr_pin(a.pos);
+        sgpr_pin(a.pos_stride);
+        sgpr_pin(a.kv.slot_ids);
+    }
     const int epi = EPI >= 0 ? EPI : sh.epi;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *s_op = smem;
