@@ -102,6 +102,27 @@ template <int EPI, int RPT, int FS>
 __global__ __launch_bounds__(256) void k_gemv_b_finish(GemvArgs a, int splits, int ss_count)
 {
 #pragma clang fp contract(off)
+    // the arguments of the partial-sum and epilogue-input loads, fetched in
+    // one round trip
+    sgpr_pin(a.w.rows);
+    sgpr_pin(a.n);
+    sgpr_pin(a.part);
+    sgpr_pin(splits);
+    sgpr_pin(ss_count);
+    sgpr_pin(a.in.ss);
+    sgpr_pin(a.in.ss_stride);
+    sgpr_pin(a.in.q);
+    sgpr_pin(a.in.tail);
+    sgpr_pin(a.out);
+    sgpr_pin(a.out_stride);
+    if constexpr (EPI == EPI_RESID) sgpr_pin(a.res);
+    if constexpr (EPI == EPI_QKV) {
+        sgpr_pin(a.kv.layer_off);
+        sgpr_pin(a.kv.slot_ids);
+        sgpr_pin(a.pos);
+        sgpr_pin(a.pos_stride);
+        sgpr_pin(a.pos0);
+    }
     const int v = blockIdx.y, l = threadIdx.x & 63;
     const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 * RPT;   // the wave's first row
     if (r0 >= a.w.rows) return;   // whole waves past the matrix

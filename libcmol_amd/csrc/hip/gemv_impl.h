@@ -303,6 +303,8 @@ void k_gemv(GemvArgs a, GemvShape sh)
     sgpr_pin(a.in.ss);
     sgpr_pin(a.in.ss_count);
     sgpr_pin(a.in.ss_stride);
+    sgpr_pin(a.in.eps);
+    sgpr_pin(a.in.tail);
     sgpr_pin(sh.qpc);
     sgpr_pin(sh.zslot);
     sgpr_pin(a.out);
@@ -1007,6 +1009,25 @@ template <int DT, int U, int EPI, int NWB = GB16_NW>
 __global__ __launch_bounds__(NWB * 64) void k_gemv_b16(GemvArgs a, int groups, int rblocks, int sq, int splits)
 {
 #pragma clang fp contract(off)
+    // launch arguments needed before the operand and weight loads go out,
+    // fetched in one round trip
+    sgpr_pin(a.w.qs);
+    sgpr_pin(a.w.d);
+    if constexpr (DT == DT_Q5_0 || DT == DT_Q6_K) sgpr_pin(a.w.qh);
+    sgpr_pin(a.w.block_quads);
+    sgpr_pin(a.w.cols);
+    sgpr_pin(a.w.row_tiles);
+    sgpr_pin(a.n);
+    sgpr_pin(a.in.q);
+    sgpr_pin(a.in.ss);
+    sgpr_pin(a.in.ss_count);
+    sgpr_pin(a.in.ss_stride);
+    sgpr_pin(a.in.eps);
+    sgpr_pin(a.in.tail);
+    sgpr_pin(groups);
+    sgpr_pin(rblocks);
+    sgpr_pin(sq);
+    sgpr_pin(splits);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int BQ = a.w.block_quads, nblk = a.w.cols >> 5, T = a.w.row_tiles;
     const int b = blockIdx.x;

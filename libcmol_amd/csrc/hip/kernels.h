@@ -191,6 +191,12 @@ struct ActIn {
     const float *ss;        // partials [vector][ss_stride] or nullptr (no norm)
     int ss_count, ss_stride;
     float eps;
+    // the struct's tail dword as a field: the kernels pin it with the other
+    // arguments, so the wide argument load that fetches it beside ss_count,
+    // ss_stride and eps keeps its register live, and the next argument load
+    // cannot target that register while the wide load is still in flight
+    // (which made the compiler wait for a second round trip)
+    int tail;
 };
 
 // ---- qtensor.hip
