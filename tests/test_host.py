@@ -179,3 +179,17 @@ def test_scheduler_window_gathers_returning_callers():
     assert native.lib().cmol__sched_selftest(threads, steps, 20000, 300, 200, native.ptr(st)) == 0
     batches = int(st[0])
     assert batches <= steps + threads + 4
+
+
+def test_scheduler_posts_wake_no_waiter_early():
+    """32 callers, a short window and long device steps: a posted step must
+    not wake the other waiters (each would re-check, and a leader woken
+    before the set is complete runs a partial batch). Batches stay near the
+    step count of the longest-lived caller (91 here); waking every waiter on
+    each post gave about 160."""
+    threads, steps = 32, 60
+    st = np.zeros(3, np.uint64)
+    assert native.lib().cmol__sched_selftest(threads, steps, 200, 4500, 0, native.ptr(st)) == 0
+    batches, total = int(st[0]), int(st[1])
+    assert total == sum(steps + i for i in range(threads))
+    assert batches <= steps + threads - 1 + 25
