@@ -138,7 +138,9 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
 #pragma unroll
             for (int e = 0; e < PE; e++) q[hh][i * PE + e] = ldg(qh + (j + 4 * i) * PE + e);
     }
-    const float scale = 1.0f / sqrtf((float)DH);
+    // scores and m stay raw dot products; a weight is 2^((t - m) c) with
+    // c = log2(e)/sqrt(d_head) on the hardware exponential (exp2(-inf) = 0)
+    const float scale = 1.0f / sqrtf((float)DH), c2 = scale * 1.44269504088896341f;
 
     fetch(0);
     put(0);
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
                 }
                 dot += __shfl_xor(dot, 1, 64);
                 dot += __shfl_xor(dot, 2, 64);
-                sc[pw] = (16 * ps + (lane >> 2)) < np ? dot * scale : -INFINITY;
+                sc[pw] = (16 * ps + (lane >> 2)) < np ? dot : -INFINITY;   // raw score
             }
             float mc = sc[0];
 #pragma unroll
@@ -188,11 +190,11 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
             float ev[PSW], ls = 0.0f;
 #pragma unroll
             for (int pw = 0; pw < PSW; pw++) {
-                ev[pw] = expf(sc[pw] - mn);
+                ev[pw] = __builtin_amdgcn_exp2f((sc[pw] - mn) * c2);
                 if (j == 0) ls += ev[pw];
             }
             ls = wave_sum(ls);
-            const float al = expf(m[hh] - mn);
+            const float al = __builtin_amdgcn_exp2f((m[hh] - mn) * c2);
             l[hh] = l[hh] * al + ls;
             m[hh] = mn;
 #pragma unroll
@@ -247,8 +249,8 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
         if (half == 1) return;
         if (nh) {
             const float m1 = xm[hw], M = fmaxf(m[0], m1);
-            const float a0 = m[0] == -INFINITY ? 0.0f : expf(m[0] - M);
-            const float a1 = m1 == -INFINITY ? 0.0f : expf(m1 - M);
+            const float a0 = m[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m[0] - M) * c2);
+            const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - M) * c2);
             l[0] = l[0] * a0 + xl[hw] * a1;
             m[0] = M;
 #pragma unroll
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_h(AttnArgs a)
             }
         }
         if (!single && lane == 0) {
-            a.pm[sbase + g] = m[hh];
+            a.pm[sbase + g] = m[hh] * scale;   // natural units, as the merge reads them
             a.pl[sbase + g] = l[hh];
         }
     }
