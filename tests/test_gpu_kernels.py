@@ -260,7 +260,9 @@ def test_gemv_reference_kats(ctx):
     (16, 4, 128, [4096, 1, 257, 1500], 256, 1), (4, 4, 128, [513, 64], 256, 1),
     (8, 4, 64, [77, 700], 256, 1), (8, 8, 256, [200, 77], 128, 1), (16, 2, 128, [1000, 3], 320, 1),
     # splits of 32-position chunks (single-session decode): head-per-wave kernel
-    (16, 4, 128, [2048, 1, 31, 33, 97], 32, 0), (9, 3, 64, [100, 2], 32, 1), (16, 4, 128, [700, 65], 96, 1)])
+    (16, 4, 128, [2048, 1, 31, 33, 97], 32, 0), (9, 3, 64, [100, 2], 32, 1), (16, 4, 128, [700, 65], 96, 1),
+    # a long context: 79 splits in one merge
+    (4, 2, 128, [5000, 40], 64, 0)])
 def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16):
     """Ragged lengths across splits of one or several 64- (or 32-) position
     chunks, fp32 and fp16 caches (the oracle reads the same rounded fp16
