@@ -296,11 +296,11 @@ def test_attention_matches_oracle(ctx, gpu, n_heads, n_kv, d_head, lens, split, 
         assert_close(got[i], want, f"attention session {i} len {L} split {split}")
 
 
-def attention_case(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16, seed):
+def attention_case(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16, seed, q_scale=1.0):
     n = len(lens)
     max_ctx = max(lens)
     rng = np.random.default_rng(seed)
-    q = rng.standard_normal((n, n_heads * d_head)).astype(np.float32)
+    q = (rng.standard_normal((n, n_heads * d_head)) * q_scale).astype(np.float32)
     kc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
     vc = rng.standard_normal((n, n_kv, max_ctx, d_head)).astype(np.float32)
     if kv_f16:
@@ -337,6 +337,24 @@ BAL_CASES = [
     (4, 2, 64, [int(x) for x in _R.integers(1, 300, 70)], 64, None),
     (16, 4, 128, [int(x) for x in _R.integers(400, 3000, 9)], 128, "48"),
 ]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d_head,lens,split,kv_f16,bal", [
+    (16, 4, 128, [4096, 1, 257, 1500], 256, 1, None),   # balanced ranges
+    (16, 4, 128, [4096, 1, 257, 1500], 256, 1, "0"),    # fp16 split grid
+    (8, 4, 64, [900, 33, 2], 64, 1, None),
+    (16, 4, 128, [2048, 5, 700], 64, 0, None),          # fp32 cache: head-per-wave kernel
+    (9, 3, 64, [1000, 65], 64, 0, None)])
+def test_attention_peaked_scores_match_oracle(ctx, gpu, monkeypatch, n_heads, n_kv, d_head, lens, split, kv_f16, bal):
+    """Queries scaled by 8 (score standard deviation 8 instead of 1): the
+    running maximum moves often and far (the lazily rescaled softmax of the
+    fp16 kernels rescales many times), and most weights underflow on the
+    hardware exponential; every kernel still matches the oracle."""
+    if bal is None:
+        monkeypatch.delenv("CMOL_ATTN_BAL", raising=False)
+    else:
+        monkeypatch.setenv("CMOL_ATTN_BAL", bal)
+    attention_case(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16, seed=len(lens) * 17 + d_head, q_scale=8.0)
 
 
 @pytest.mark.parametrize("n_heads,n_kv,d_head,lens,split,bal", BAL_CASES)
