@@ -323,6 +323,34 @@ def attention_case(ctx, gpu, n_heads, n_kv, d_head, lens, split, kv_f16, seed, q
         assert_close(got[i], want, f"attention session {i} len {L} split {split}")
 
 
+def test_attention_decode_rejects_bad_arguments(ctx, gpu):
+    """Shapes the decode attention cannot take fail with an error code before
+    any attention kernel runs: no vectors, query heads not a multiple of the
+    kv heads, splits that are not whole 32-position chunks (or 32-position
+    chunks at a d_head other than 64 / 128), a d_head without a kernel and
+    more than 8 query heads per kv head; a valid call afterwards still
+    matches the oracle."""
+    import ctypes as C
+    L = gpu.lib()
+    dq = ctx.upload(np.zeros(16 * 256, np.float32))
+    dk = ctx.upload(np.zeros(4 * 64 * 256, np.float32))
+    dv = ctx.upload(np.zeros(4 * 64 * 256, np.float32))
+    ds = ctx.upload(np.array([10], np.int32))
+    dout = ctx.alloc(16 * 256 * 4)
+
+    def call(n, n_heads, n_kv, d_head, split):
+        return L.cmolhip_attn_decode(ctx.h, n, C.c_void_p(dq), C.c_void_p(dk), C.c_void_p(dv), C.c_void_p(ds),
+                                     n_heads, n_kv, d_head, 64, 0, split, C.c_void_p(dout))
+
+    assert call(0, 4, 4, 64, 64) == gpu.CMOL_ERR_ARGS        # no vectors
+    assert call(1, 6, 4, 64, 64) == gpu.CMOL_ERR_ARGS        # 6 query heads over 4 kv heads
+    assert call(1, 4, 4, 64, 48) == gpu.CMOL_ERR_ARGS        # not whole 32-position chunks
+    assert call(1, 4, 4, 256, 32) == gpu.CMOL_ERR_ARGS       # 32-position chunks at d_head 256
+    assert call(1, 4, 4, 48, 64) == gpu.CMOL_ERR_UNSUPPORTED  # no d_head 48 kernel
+    assert call(1, 16, 1, 16, 64) == gpu.CMOL_ERR_UNSUPPORTED  # 16 query heads per kv head
+    attention_case(ctx, gpu, 8, 2, 64, [10, 3], 64, 0, seed=5)
+
+
 # Balanced ranges over an fp16 cache: CMOL_ATTN_BAL = total work-groups, so
 # bal = total / n_kv - n ranges per kv head (at most n * (splits - 1)); small
 # grids cut contexts into several pieces (and ranges across several
